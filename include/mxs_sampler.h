@@ -1,0 +1,118 @@
+/*
+ * mxs_sampler.h -- C ABI of the MI355X (gfx950) sampler chain.
+ *
+ * One call samples a whole batch of logits rows on the GPU:
+ *   repetition penalty -> greedy (T == 0) -> temperature -> top-k -> top-p
+ *   -> softmax -> draw,
+ * the chain of mini_engine/sampling.py:30-69, with per-row parameters passed
+ * as device arrays.  Plain pointers and sizes only; every buffer belongs to
+ * the caller and the library allocates nothing.  Calls are asynchronous and
+ * ordered on `stream`.  Two calls may run concurrently only with distinct
+ * workspaces.
+ *
+ * Results per row (token ids, post-filter probabilities) are defined by the
+ * exact arithmetic described in the oracle that the tests check against:
+ * integer softmax masses floor(exp(l - m) * 2^44), exact top-p and draw
+ * thresholds, ties in value broken by the lowest index, and an inverse-CDF
+ * draw (in sorted order) from one uniform per row in place of
+ * torch.multinomial's exponential race.
+ */
+#ifndef MXS_SAMPLER_H
+#define MXS_SAMPLER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* HIP stream handle; identical to hipStream_t from <hip/hip_runtime_api.h>. */
+typedef struct ihipStream_t* mxs_stream_t;
+
+/* Logits element types (sampling.py:36 upcasts fp16 rows to fp32). */
+enum mxs_dtype {
+    MXS_DTYPE_F32 = 0,
+    MXS_DTYPE_F16 = 1
+};
+
+/* Return codes of the calls below. */
+enum mxs_status {
+    MXS_OK = 0,
+    MXS_ERR_INVALID_ARGUMENT = 1,  /* bad shape, dtype or null pointer */
+    MXS_ERR_ALIGNMENT = 2,         /* logits not element-aligned or workspace not 256-byte aligned */
+    MXS_ERR_WORKSPACE_TOO_SMALL = 3,
+    MXS_ERR_VOCAB_TOO_LARGE = 4,   /* V > MXS_MAX_VOCAB */
+    MXS_ERR_HIP = 5                /* a HIP runtime call failed */
+};
+
+/* Per-row outcome written to out_status (out_tokens holds -1 unless OK). */
+enum mxs_row_status {
+    MXS_ROW_OK = 0,
+    MXS_ROW_BAD_HISTORY = 1,    /* a history id is outside [0, V) (torch: IndexError) */
+    MXS_ROW_BAD_PARAM = 2,      /* temperature is NaN */
+    MXS_ROW_NONFINITE = 3,      /* max tempered logit is inf/NaN (torch: multinomial error) */
+    MXS_ROW_EMPTY_NUCLEUS = 4   /* top_p <= 0 removes every token (torch: multinomial error) */
+};
+
+#define MXS_MAX_VOCAB 262144
+
+/* Library version string, e.g. "mxs-sampler 0.1.0 gfx950". */
+const char* mxs_version(void);
+
+/* Human-readable text for an mxs_status value. */
+const char* mxs_status_string(int status);
+
+/*
+ * Workspace size in bytes for a batch of B rows of V logits.  The workspace
+ * starts with a control area of mxs_control_bytes(B) bytes (per-row arrival
+ * counters) followed by the rows' top-k candidate lists.  It must be 256-byte
+ * aligned.  The control area must be zero when mxs_sample starts, and every
+ * call leaves it zero again, so consecutive calls with the same B need no
+ * re-initialization.  A call with a different B writes candidates where the
+ * other B's control area lies: zero the control area (mxs_workspace_init with
+ * bytes = mxs_control_bytes(B)) before the first call and whenever B changes.
+ */
+size_t mxs_workspace_bytes(int B, int V);
+
+/* Size of the control area at the start of the workspace for B rows. */
+size_t mxs_control_bytes(int B);
+
+/* Zero the first `bytes` bytes of a workspace on `stream` (a fill kernel, so
+ * no memset node is recorded if the caller captures the stream). */
+int mxs_workspace_init(void* workspace, size_t bytes, mxs_stream_t stream);
+
+/*
+ * Sample one token per row.  Replaces the per-row Python call
+ * sample(logits[i], params, generated_ids, generator) of
+ * mini_engine/sampling.py:30-69 as called from mini_engine/scheduler.py:268-275.
+ *
+ *   logits        [B, ld] device array of dtype `dtype`; row r uses the first V
+ *                 elements.  Rows that start on a 16-byte boundary are read
+ *                 with 128-bit loads, other rows element by element.
+ *   temperature   f32[B]  0 => greedy argmax (sampling.py:25-27, 47-48)
+ *   top_k         i32[B]  <= 0 => off (sampling.py:52)
+ *   top_p         f32[B]  >= 1 or NaN => off (sampling.py:56)
+ *   penalty       f32[B]  1 => off (sampling.py:38)
+ *   hist_offsets  i32[B+1] CSR offsets into hist_ids, or NULL for no history
+ *   hist_ids      i32[hist_offsets[B]] generated token ids (any order, repeats ok)
+ *   uniforms      f32[B]  one u in [0,1) per row (clamped into it), or NULL for u = 0
+ *   out_tokens    i64[B]  sampled ids; -1 for rows whose status is not MXS_ROW_OK
+ *   out_status    i32[B]  mxs_row_status per row, or NULL
+ *   out_probs     f32[B, V] post-filter probabilities (sampling.py:68), or NULL.
+ *                 Greedy rows get a one-hot row.
+ *   workspace     device buffer of at least mxs_workspace_bytes(B, V) bytes
+ */
+int mxs_sample(const void* logits, int dtype, int B, int V, int64_t ld,
+               const float* temperature, const int32_t* top_k,
+               const float* top_p, const float* penalty,
+               const int32_t* hist_offsets, const int32_t* hist_ids,
+               const float* uniforms,
+               int64_t* out_tokens, int32_t* out_status, float* out_probs,
+               void* workspace, size_t workspace_bytes, mxs_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MXS_SAMPLER_H */

@@ -1,0 +1,272 @@
+// mxs_device.h -- device building blocks of the gfx950 sampler kernels.
+//
+// Everything here runs inside one 512-thread workgroup (8 wave64s).  The
+// arithmetic helpers (keys, mass, exact thresholds) are the same operation
+// sequences the CPU oracle uses, so results agree bit for bit; the file must
+// be compiled with -ffp-contract=off so that the only fused multiply-adds are
+// the explicit __builtin_fmaf calls.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mxs {
+
+typedef unsigned long long u64;
+typedef unsigned __int128 u128;
+
+constexpr int NT = 512;                 // threads per workgroup
+constexpr int NWAVES = NT / 64;
+constexpr int CS_MAX = 16384;           // logits staged in LDS per chunk
+constexpr int CS_MIN = 2048;
+constexpr int KMAX = 1024;              // largest top_k served by the candidate path
+constexpr int CHUNK_CAP = 2048;         // candidates one chunk may emit
+constexpr int SORT_CAP = 4096;          // top-k survivors sorted in LDS (= 8 per thread)
+constexpr int LCAP = 2048;              // elements collected per refinement step (= 4 per thread)
+constexpr int MASS_SHIFT = 20;          // masses carry 44 fractional bits: 24-bit P << (20 + n)
+constexpr uint32_t SK_MIN = 0x007FFFFFu;  // selection key of -inf (T > 0) or +inf (T < 0)
+
+// LDS map of the sampling kernel (dynamic shared memory).
+constexpr int LDS_REGION = 65536;       // chunk logits / sort buffers / row bitmap
+constexpr int LDS_HIST = LDS_REGION;    // 2048 x u32 radix histogram
+constexpr int LDS_BM = LDS_HIST + 8192; // 512 x u32 chunk penalty bitmap
+constexpr int LDS_BYTES = LDS_BM + 2048;
+
+__host__ __device__ __forceinline__ uint32_t f2u(float f) { return __builtin_bit_cast(uint32_t, f); }
+__host__ __device__ __forceinline__ float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
+
+// Order-preserving key: a < b (non-NaN)  =>  okey(a) < okey(b).
+__host__ __device__ __forceinline__ uint32_t okey(float f)
+{
+    uint32_t u = f2u(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__host__ __device__ __forceinline__ float okey_inv(uint32_t k)
+{
+    return u2f((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+// Value key: -0 and +0 compare equal, so they share the key of +0.
+__host__ __device__ __forceinline__ uint32_t vkey(float f) { return okey(f == 0.0f ? 0.0f : f); }
+
+// Selection key of a penalized logit x: ordered like x / T (reversed for T < 0).
+__device__ __forceinline__ uint32_t selkey(float x, bool neg)
+{
+    uint32_t k = okey(x);
+    return neg ? ~k : k;
+}
+__device__ __forceinline__ float sel_inv(uint32_t s, bool neg) { return okey_inv(neg ? ~s : s); }
+
+// Integer softmax numerator of d = fl32(l - m) <= 0: floor(exp(d) * 2^44), with
+// exp evaluated as 2^n * q(r): n = rint(d log2 e), r = d - n ln2 (Cody-Waite,
+// two fma), q = degree-7 Taylor polynomial of exp(r) in Horner form.
+__host__ __device__ __forceinline__ u64 mass_of(float d)
+{
+    if (!(d >= -104.0f)) return 0;
+    float t = d * 0x1.715476p+0f;
+    float n = __builtin_rintf(t);
+    float r = __builtin_fmaf(n, -0x1.62e4p-1f, d);
+    r = __builtin_fmaf(n, -0x1.7f7d1cp-20f, r);
+    float q = 0x1.a01a02p-13f;
+    q = __builtin_fmaf(q, r, 0x1.6c16c2p-10f);
+    q = __builtin_fmaf(q, r, 0x1.111112p-7f);
+    q = __builtin_fmaf(q, r, 0x1.555556p-5f);
+    q = __builtin_fmaf(q, r, 0x1.555556p-3f);
+    q = __builtin_fmaf(q, r, 0.5f);
+    q = __builtin_fmaf(q, r, 1.0f);
+    q = __builtin_fmaf(q, r, 1.0f);
+    uint32_t P = (uint32_t)(q * 16777216.0f);
+    int s = MASS_SHIFT + (int)n;
+    if (s >= 0) return (u64)P << s;
+    if (s <= -26) return 0;
+    return (u64)(P >> (-s));
+}
+
+// v in [0, 1) as M * 2^-sh, M < 2^24.
+__host__ __device__ __forceinline__ void split_unit(float v, uint32_t& M, int& sh)
+{
+    uint32_t b = f2u(v), e = (b >> 23) & 0xFFu, f = b & 0x7FFFFFu;
+    if (e == 0) { M = f; sh = 149; }
+    else        { M = f | 0x800000u; sh = 150 - (int)e; }
+}
+
+// ceil(p * W) for 0 < p < 1, exact.
+__host__ __device__ __forceinline__ u64 ceil_mul(float p, u64 W)
+{
+    uint32_t M; int sh;
+    split_unit(p, M, sh);
+    u128 prod = (u128)M * W;
+    if (prod == 0) return 0;
+    if (sh >= 100) return 1;
+    u128 one = (u128)1 << sh;
+    return (u64)((prod + one - 1) >> sh);
+}
+
+// floor(u * W) for 0 <= u < 1, exact.
+__host__ __device__ __forceinline__ u64 floor_mul(float u, u64 W)
+{
+    uint32_t M; int sh;
+    split_unit(u, M, sh);
+    if (sh >= 100) return 0;
+    return (u64)(((u128)M * W) >> sh);
+}
+
+__host__ __device__ __forceinline__ float clamp_uniform(float u)
+{
+    if (!(u >= 0.0f)) return 0.0f;
+    if (u >= 1.0f) return 0x1.fffffep-1f;
+    return u;
+}
+
+// ---------------------------------------------------------------- wave/block
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+
+__device__ __forceinline__ u64 wave_max_u64(u64 v)
+{
+    for (int o = 32; o > 0; o >>= 1) {
+        u64 w = __shfl_xor(v, o, 64);
+        v = w > v ? w : v;
+    }
+    return v;
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
+{
+    for (int o = 32; o > 0; o >>= 1) {
+        uint32_t w = __shfl_xor(v, o, 64);
+        v = w > v ? w : v;
+    }
+    return v;
+}
+
+// Number of set bits of `mask` below this lane.
+__device__ __forceinline__ uint32_t lanes_below(u64 mask)
+{
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                     __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+template <typename T>
+__device__ __forceinline__ T block_sum(T v)
+{
+    __shared__ T s[NWAVES];
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    __syncthreads();
+    if (lane_id() == 0) s[wave_id()] = v;
+    __syncthreads();
+    T t = 0;
+#pragma unroll
+    for (int i = 0; i < NWAVES; ++i) t += s[i];
+    return t;
+}
+
+// Inclusive scan of one value per thread, in thread order; *total gets the sum.
+template <typename T>
+__device__ __forceinline__ T block_incl_scan(T v, T* total)
+{
+    __shared__ T s[NWAVES];
+    const int lane = lane_id(), w = wave_id();
+    for (int o = 1; o < 64; o <<= 1) {
+        T y = __shfl_up(v, o, 64);
+        if (lane >= o) v += y;
+    }
+    __syncthreads();
+    if (lane == 63) s[w] = v;
+    __syncthreads();
+    T off = 0, tot = 0;
+#pragma unroll
+    for (int i = 0; i < NWAVES; ++i) {
+        if (i < w) off += s[i];
+        tot += s[i];
+    }
+    *total = tot;
+    return v + off;
+}
+
+struct BinHit {
+    int bin;
+    u64 above;   // sum of the bins above `bin`
+};
+
+// Descending search over h[0..nb): the bin b with  above(b) <= t < above(b) + h[b],
+// where above(b) = sum of h over bins > b.  nb must be a multiple of NT.
+template <typename T>
+__device__ BinHit find_desc(const T* h, int nb, u64 t)
+{
+    __shared__ BinHit s_hit;
+    const int per = nb / NT;
+    const int b0 = threadIdx.x * per;
+    if (threadIdx.x == 0) s_hit = BinHit{0, 0};   // ordered before the search by the scan's barriers
+    u64 mine = 0;
+    for (int i = 0; i < per; ++i) mine += (u64)h[b0 + i];
+    u64 total;
+    u64 incl = block_incl_scan<u64>(mine, &total);
+    u64 a = total - incl;   // mass of bins above this thread's range
+    for (int b = b0 + per - 1; b >= b0; --b) {
+        u64 hb = (u64)h[b];
+        if (a <= t && t < a + hb) s_hit = BinHit{b, a};
+        a += hb;
+    }
+    __syncthreads();
+    BinHit r = s_hit;
+    __syncthreads();
+    return r;
+}
+
+// kk-th largest (1-based) 32-bit key among key(i), i in [0, n), by an MSD radix
+// select with digits of 11, 11 and 10 bits and a 2048-entry LDS histogram.
+// When the bin holding the answer has at most `small` keys the search stops
+// and returns that bin's lower edge (a valid lower bound); small = 0 gives the
+// exact key.
+template <class KeyF>
+__device__ uint32_t block_select_desc(int n, uint32_t kk, KeyF key, uint32_t* hist, uint32_t small)
+{
+    const int shifts[3] = {21, 10, 0};
+    const int widths[3] = {11, 11, 10};
+    uint32_t prefix = 0;
+    for (int lev = 0; lev < 3; ++lev) {
+        const int sh = shifts[lev], nb = 1 << widths[lev];
+        const int hsh = sh + widths[lev];
+        for (int b = threadIdx.x; b < nb; b += NT) hist[b] = 0;
+        __syncthreads();
+        for (int i = threadIdx.x; i < n; i += NT) {
+            uint32_t k = key(i);
+            if (lev == 0 || (k >> hsh) == prefix) atomicAdd(&hist[(k >> sh) & (nb - 1)], 1u);
+        }
+        __syncthreads();
+        BinHit hit = find_desc<uint32_t>(hist, nb, (u64)(kk - 1));
+        kk -= (uint32_t)hit.above;
+        prefix = (prefix << widths[lev]) | (uint32_t)hit.bin;
+        uint32_t cnt = hist[hit.bin];
+        __syncthreads();
+        if (cnt <= small || lev == 2) return prefix << sh;
+    }
+    return prefix;
+}
+
+// Bitonic sort of P (power of two) u64 keys in LDS, descending.
+__device__ __forceinline__ void bitonic_sort_desc(u64* a, int P)
+{
+    for (int k = 2; k <= P; k <<= 1) {
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int i = threadIdx.x; i < P; i += NT) {
+                int ixj = i ^ j;
+                if (ixj > i) {
+                    u64 x = a[i], y = a[ixj];
+                    bool up = (i & k) != 0;   // this sub-block ascends
+                    if (up ? (x > y) : (x < y)) { a[i] = y; a[ixj] = x; }
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+__device__ __forceinline__ int pow2_ceil(int n)
+{
+    int p = 1;
+    while (p < n) p <<= 1;
+    return p;
+}
+
+}  // namespace mxs

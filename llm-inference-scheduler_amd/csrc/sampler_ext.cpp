@@ -1,0 +1,123 @@
+// sampler_ext.cpp -- thin PyTorch-ROCm extension over the C ABI (mxs_sampler.h).
+//
+// It checks tensor dtypes, shapes, devices and contiguity, takes torch's
+// current HIP stream for the logits' device and forwards raw pointers to
+// mxs_sample.  No compute happens here and nothing is allocated: the Python
+// layer (mi355x_sampler.batch) owns outputs and the workspace.
+#include <torch/extension.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+
+#include <optional>
+#include <sstream>
+#include <string>
+
+#include "mxs_sampler.h"
+
+namespace {
+
+void check_dev(const torch::Tensor& t, const torch::Tensor& ref, const char* name,
+               c10::ScalarType dt, int64_t numel)
+{
+    TORCH_CHECK(t.device() == ref.device(), name, " must be on ", ref.device(), ", got ", t.device());
+    TORCH_CHECK(t.scalar_type() == dt, name, " must be ", c10::toString(dt), ", got ", t.scalar_type());
+    TORCH_CHECK(t.is_contiguous(), name, " must be contiguous");
+    if (numel >= 0) TORCH_CHECK(t.numel() == numel, name, " must have ", numel, " elements, got ", t.numel());
+}
+
+const void* opt_ptr(const std::optional<torch::Tensor>& t) { return t ? t->data_ptr() : nullptr; }
+
+void raise_status(int st, const char* what)
+{
+    if (st == MXS_OK) return;
+    std::ostringstream os;
+    os << what << " failed: " << mxs_status_string(st) << " (status " << st << ")";
+    if (st == MXS_ERR_INVALID_ARGUMENT || st == MXS_ERR_VOCAB_TOO_LARGE || st == MXS_ERR_ALIGNMENT)
+        throw std::invalid_argument(os.str());
+    throw std::runtime_error(os.str());
+}
+
+}  // namespace
+
+int64_t workspace_bytes(int64_t B, int64_t V)
+{
+    return (int64_t)mxs_workspace_bytes((int)B, (int)V);
+}
+
+int64_t control_bytes(int64_t B) { return (int64_t)mxs_control_bytes((int)B); }
+
+void workspace_init(torch::Tensor ws)
+{
+    TORCH_CHECK(ws.is_cuda() && ws.is_contiguous() && ws.scalar_type() == torch::kUInt8,
+                "workspace must be a contiguous uint8 device tensor");
+    const c10::DeviceGuard guard(ws.device());
+    auto stream = c10::hip::getCurrentHIPStream();
+    raise_status(mxs_workspace_init(ws.data_ptr(), (size_t)ws.numel(), (mxs_stream_t)stream.stream()),
+                 "mxs_workspace_init");
+}
+
+void sample(torch::Tensor logits, torch::Tensor temperature, torch::Tensor top_k,
+            torch::Tensor top_p, torch::Tensor penalty,
+            std::optional<torch::Tensor> hist_offsets, std::optional<torch::Tensor> hist_ids,
+            std::optional<torch::Tensor> uniforms, torch::Tensor out_tokens,
+            std::optional<torch::Tensor> out_status, std::optional<torch::Tensor> out_probs,
+            torch::Tensor workspace)
+{
+    TORCH_CHECK(logits.is_cuda(), "logits must be on a GPU device");
+    TORCH_CHECK(logits.dim() == 2, "logits must be [B, V]");
+    TORCH_CHECK(logits.stride(1) == 1, "logits rows must be contiguous");
+    const int64_t B = logits.size(0), V = logits.size(1);
+    int dtype;
+    if (logits.scalar_type() == torch::kFloat32) dtype = MXS_DTYPE_F32;
+    else if (logits.scalar_type() == torch::kFloat16) dtype = MXS_DTYPE_F16;
+    else TORCH_CHECK(false, "logits must be float32 or float16, got ", logits.scalar_type());
+
+    check_dev(temperature, logits, "temperature", torch::kFloat32, B);
+    check_dev(top_k, logits, "top_k", torch::kInt32, B);
+    check_dev(top_p, logits, "top_p", torch::kFloat32, B);
+    check_dev(penalty, logits, "penalty", torch::kFloat32, B);
+    TORCH_CHECK(hist_offsets.has_value() == hist_ids.has_value(),
+                "hist_offsets and hist_ids go together");
+    if (hist_offsets) {
+        check_dev(*hist_offsets, logits, "hist_offsets", torch::kInt32, B + 1);
+        check_dev(*hist_ids, logits, "hist_ids", torch::kInt32, -1);
+    }
+    if (uniforms) check_dev(*uniforms, logits, "uniforms", torch::kFloat32, B);
+    check_dev(out_tokens, logits, "out_tokens", torch::kInt64, B);
+    if (out_status) check_dev(*out_status, logits, "out_status", torch::kInt32, B);
+    if (out_probs) check_dev(*out_probs, logits, "out_probs", torch::kFloat32, B * V);
+    TORCH_CHECK(workspace.device() == logits.device() && workspace.is_contiguous() &&
+                workspace.scalar_type() == torch::kUInt8, "workspace must be a uint8 tensor on the logits device");
+
+    const c10::DeviceGuard guard(logits.device());
+    auto stream = c10::hip::getCurrentHIPStream();
+    const int32_t* hoff = hist_offsets ? hist_offsets->data_ptr<int32_t>() : nullptr;
+    // An empty id list may have no storage; any valid pointer will do since
+    // the offsets then select no ids.
+    const int32_t* hids = nullptr;
+    if (hist_ids) hids = hist_ids->numel() ? hist_ids->data_ptr<int32_t>() : hoff;
+    int st = mxs_sample(logits.data_ptr(), dtype, (int)B, (int)V, logits.stride(0),
+                        temperature.data_ptr<float>(), top_k.data_ptr<int32_t>(),
+                        top_p.data_ptr<float>(), penalty.data_ptr<float>(), hoff, hids,
+                        (const float*)opt_ptr(uniforms), out_tokens.data_ptr<int64_t>(),
+                        out_status ? out_status->data_ptr<int32_t>() : nullptr,
+                        out_probs ? out_probs->data_ptr<float>() : nullptr,
+                        workspace.data_ptr(), (size_t)workspace.numel(),
+                        (mxs_stream_t)stream.stream());
+    raise_status(st, "mxs_sample");
+}
+
+std::string version() { return mxs_version(); }
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m)
+{
+    m.doc() = "MI355X sampler chain: torch front end of the mxs_sampler C ABI";
+    m.def("version", &version);
+    m.def("workspace_bytes", &workspace_bytes, "workspace size for a [B, V] batch");
+    m.def("control_bytes", &control_bytes, "size of the workspace control area for B rows");
+    m.def("workspace_init", &workspace_init, "zero a workspace (or its control area) on the current stream");
+    m.def("sample", &sample, "sample one token per row (see mxs_sampler.h)",
+          py::arg("logits"), py::arg("temperature"), py::arg("top_k"), py::arg("top_p"),
+          py::arg("penalty"), py::arg("hist_offsets"), py::arg("hist_ids"), py::arg("uniforms"),
+          py::arg("out_tokens"), py::arg("out_status"), py::arg("out_probs"), py::arg("workspace"));
+}

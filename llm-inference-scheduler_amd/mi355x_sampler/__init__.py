@@ -1,0 +1,18 @@
+"""MI355X-native sampler chain (repetition penalty, greedy, temperature,
+top-k, top-p, softmax, draw) for the reference engine's
+mini_engine/sampling.py, on hand-written gfx950 HIP kernels.
+
+  SamplingParams, sample   drop-in for mini_engine/sampling.py:15-69
+  sample_batch             one launch for a [B, V] batch, per-row device params
+  sample_requests          batch from per-request SamplingParams / histories
+"""
+
+from .batch import (MAX_VOCAB, ROW_BAD_HISTORY, ROW_BAD_PARAM, ROW_EMPTY_NUCLEUS,
+                    ROW_NONFINITE, ROW_OK, pack_requests, sample_batch, sample_requests)
+from .sampling import SamplingParams, sample
+
+__all__ = [
+    "SamplingParams", "sample", "sample_batch", "sample_requests", "pack_requests",
+    "MAX_VOCAB", "ROW_OK", "ROW_BAD_HISTORY", "ROW_BAD_PARAM", "ROW_NONFINITE",
+    "ROW_EMPTY_NUCLEUS",
+]

@@ -1,0 +1,182 @@
+"""GPU sampler vs the CPU oracle: identical token ids and row statuses,
+post-filter probabilities within 1e-6 absolute (the
+kernels use the oracle's arithmetic, so they are normally bit-identical).
+
+Every launch goes through mi355x_sampler.sample_batch -> torch extension ->
+mxs_sample (C ABI) -> gfx950 kernels.
+"""
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from mi355x_sampler import sample_batch
+from mi355x_sampler.workloads import VOCAB, Workload, make_workload
+
+pytestmark = pytest.mark.gpu
+
+PROB_TOL = 1e-6
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def run_gpu(w: Workload, device, probs=True):
+    d = w.to_device(device)
+    out = torch.zeros((w.B, w.V), dtype=torch.float32, device=device) if probs else None
+    tok, st = sample_batch(**d, out_probs=out, return_status=True)
+    torch.cuda.synchronize()
+    return tok.cpu().numpy(), st.cpu().numpy(), (out.cpu().numpy() if probs else None)
+
+
+def run_oracle(oracle, w: Workload, probs=True):
+    return oracle.sample_rows(w.logits, w.temperature, w.top_k, w.top_p, w.penalty,
+                              w.hist_offsets, w.hist_ids, w.uniforms, want_probs=probs)
+
+
+def check(w, ref, tok, st, probs):
+    assert np.array_equal(st, ref.status), f"status gpu {st[:16]} oracle {ref.status[:16]}"
+    bad = np.nonzero(tok != ref.tokens)[0]
+    assert bad.size == 0, (f"{w.name}: token mismatch in {bad.size} rows, first {bad[:8]}: "
+                           f"gpu {tok[bad[:8]]} oracle {ref.tokens[bad[:8]]}")
+    if probs is not None:
+        err = np.abs(probs - ref.probs)
+        worst = np.unravel_index(int(err.argmax()), err.shape)
+        assert err.max() <= PROB_TOL, f"{w.name}: |dprob| {err.max()} at {worst}"
+
+
+def custom(name, logits, T, k, p, pen, hists, u):
+    x = np.ascontiguousarray(np.atleast_2d(logits))
+    B = x.shape[0]
+    bc = lambda v, dt: np.broadcast_to(np.asarray(v, dtype=dt), (B,)).copy()
+    off = np.zeros(B + 1, np.int32)
+    off[1:] = np.cumsum([len(h) for h in hists])
+    ids = np.asarray([i for h in hists for i in h], dtype=np.int32)
+    return Workload(name, x, bc(T, np.float32), bc(k, np.int32), bc(p, np.float32),
+                    bc(pen, np.float32), off, ids, bc(u, np.float32))
+
+
+@pytest.mark.parametrize("name,B", [("single", 1), ("greedy", 16), ("peaked", 16),
+                                    ("zipf", 24), ("flat16", 3)])
+def test_parity_small_batches(oracle, cuda, name, B):
+    w = make_workload(name, B=B)
+    say(f"[parity-small] {name} B={B} V={w.V}")
+    ref = run_oracle(oracle, w)
+    tok, st, probs = run_gpu(w, cuda)
+    check(w, ref, tok, st, probs)
+
+
+@pytest.mark.parametrize("name", ["greedy", "peaked", "zipf"])
+def test_parity_full_batches(oracle, cuda, name):
+    w = make_workload(name)
+    say(f"[parity-full] {name} B={w.B} V={w.V}")
+    ref = run_oracle(oracle, w, probs=False)
+    tok, st, _ = run_gpu(w, cuda, probs=False)
+    check(w, ref, tok, st, None)
+
+
+def test_parity_full_flat16(oracle, cuda):
+    w = make_workload("flat16", B=64)
+    say(f"[parity-full] flat16 B={w.B} V={w.V}")
+    ref = run_oracle(oracle, w, probs=False)
+    tok, st, _ = run_gpu(w, cuda, probs=False)
+    check(w, ref, tok, st, None)
+
+
+def _edge_rows(V, seed=7):
+    rng = np.random.default_rng(seed)
+    base = (2.0 * rng.standard_normal(V)).astype(np.float32)
+    rows = []
+    #          T      k     p      pen   hist                      u
+    rows.append((0.8, 1, 1.0, 1.0, [], 0.3))                  # k = 1
+    rows.append((0.8, V, 1.0, 1.0, [], 0.3))                  # k = V keeps all
+    rows.append((0.8, V + 5, 0.5, 1.0, [], 0.7))              # k > V
+    rows.append((1.3, 0, 1e-7, 1.0, [], 0.9))                 # tiny top_p keeps the argmax
+    rows.append((-0.9, 20, 0.8, 1.0, [], 0.5))                # negative temperature
+    rows.append((0.6, 0, 1.0, 0.7, [3, 3, 5, 9, 9, 9], 0.2))  # penalty < 1, duplicates
+    rows.append((2.5, 700, 0.97, 1.2, list(range(0, V, 7)), 0.999))
+    rows.append((0.05, 40, 0.9, 1.0, [], 0.0))                # u = 0
+    rows.append((1.0, 1024, 0.99, 1.0, [], 0.61))             # k = KMAX
+    rows.append((1.0, 1025, 0.99, 1.0, [], 0.61))             # k just above KMAX
+    return base, rows
+
+
+@pytest.mark.parametrize("V", [1000, 4099, VOCAB])
+def test_parity_edge_parameters(oracle, cuda, V):
+    base, rows = _edge_rows(V)
+    x = np.stack([base] * len(rows))
+    T, k, p, pen, h, u = (list(c) for c in zip(*rows))
+    w = custom("edge", x, T, k, p, pen, h, u)
+    say(f"[edge-params] V={V} rows={w.B}")
+    ref = run_oracle(oracle, w)
+    tok, st, probs = run_gpu(w, cuda)
+    check(w, ref, tok, st, probs)
+
+
+def test_parity_ties_and_infinities(oracle, cuda):
+    V = VOCAB
+    rows, params = [], []
+    rows.append(np.zeros(V, np.float32)); params.append((0.7, 0, 0.5, 1.0, [], 0.37))      # all tied
+    rows.append(np.zeros(V, np.float32)); params.append((0.7, 50, 1.0, 1.0, [], 0.37))     # tied top-k
+    r = np.full(V, -np.inf, np.float32); r[[5, 77, 150000]] = [1.0, 2.0, 2.0]
+    rows.append(r); params.append((1.0, 0, 1.0, 1.0, [], 0.8))                             # -inf mask
+    rows.append(r.copy()); params.append((1.0, 10, 1.0, 1.0, [], 0.8))                     # kth is -inf
+    q = np.round(np.random.default_rng(3).standard_normal(V) * 4).astype(np.float32)
+    rows.append(q); params.append((0.9, 300, 0.9, 1.1, [1, 2, 3], 0.55))                   # coarse ties
+    rows.append(q.copy()); params.append((float("inf"), 0, 0.3, 1.0, [], 0.5))             # T = inf
+    T, k, p, pen, h, u = (list(c) for c in zip(*params))
+    w = custom("ties", np.stack(rows), T, k, p, pen, h, u)
+    say(f"[ties] rows={w.B}")
+    ref = run_oracle(oracle, w)
+    tok, st, probs = run_gpu(w, cuda)
+    check(w, ref, tok, st, probs)
+
+
+def test_row_status_errors(oracle, cuda):
+    V = 5000
+    x = np.random.default_rng(1).standard_normal((5, V)).astype(np.float32)
+    x[3, 17] = np.inf
+    w = custom("errors", x, [0.8, float("nan"), 0.8, 0.8, 0.8], [0, 0, 0, 0, 0],
+               [1.0, 1.0, 0.0, 1.0, 0.9], [1.2, 1.0, 1.0, 1.0, 1.0],
+               [[V + 3], [], [], [], []], [0.5] * 5)
+    say("[errors]")
+    ref = run_oracle(oracle, w)
+    tok, st, _ = run_gpu(w, cuda, probs=False)
+    assert list(ref.status) == [1, 2, 4, 3, 0]
+    check(w, ref, tok, st, None)
+
+
+def test_greedy_nan_and_ties(oracle, cuda):
+    V = 70000
+    x = np.zeros((3, V), np.float32)
+    x[0, [10, 20]] = 5.0                       # tie: lowest index
+    x[1, 30] = np.nan; x[1, 40] = np.nan       # NaN is the max, first one
+    x[2, :] = -1.0; x[2, 69999] = -0.5
+    w = custom("greedy-edge", x, 0.0, 0, 1.0, [1.0, 1.0, 2.0], [[], [], [69999]], 0.0)
+    ref = run_oracle(oracle, w)
+    tok, st, _ = run_gpu(w, cuda, probs=False)
+    assert list(ref.tokens) == [10, 30, 0]
+    check(w, ref, tok, st, None)
+
+
+def test_repeat_calls_leave_workspace_clean(oracle, cuda):
+    w = make_workload("zipf", B=8)
+    ref = run_oracle(oracle, w, probs=False)
+    for _ in range(3):
+        tok, st, _ = run_gpu(w, cuda, probs=False)
+        check(w, ref, tok, st, None)
+
+
+def test_workspace_reuse_across_batch_sizes(oracle, cuda):
+    """Candidate lists of one batch size land where another batch size keeps
+    its row counters; changing B between calls must still give exact rows."""
+    for name, B in [("peaked", 64), ("zipf", 256), ("zipf", 8), ("peaked", 64), ("zipf", 256)]:
+        w = make_workload(name, B=B)
+        say(f"[ws-reuse] {name} B={B}")
+        ref = run_oracle(oracle, w, probs=False)
+        tok, st, _ = run_gpu(w, cuda, probs=False)
+        check(w, ref, tok, st, None)
