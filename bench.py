@@ -1,0 +1,234 @@
+"""Benchmark: sampled rows/s and achieved HBM GB/s of the gfx950 sampler chain.
+
+Default workload (the headline): B=256 rows x V=151,936 fp32 logits with
+Zipf-shaped rows and heterogeneous per-row temperature, top_k, top_p and
+repetition penalty over 1024-id histories (mi355x_sampler.workloads "zipf").
+A step is one launch of the chain over the whole batch, with logits, per-row
+parameters, histories and uniforms already resident in HBM.
+
+Prints one JSON line.  `value` is rows/s over the timed steps (wall clock,
+synchronized on both sides).  `roofline` divides the algorithmic bytes of one
+launch (logits once + int32 history + 16 B of parameters + 4 B uniform per
+stochastic row + 8 B token out, per row) by the kernel's mean duration from
+HIP events recorded around each launch on the launch stream.  `cpu_baseline`
+times the torch-CPU restatement of the reference chain on a bounded sample
+of the same rows, on the host cores.
+
+  python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--workload zipf]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "llm-inference-scheduler_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBPS = 8000.0
+METRIC = "sampled rows/sec + achieved HBM GB/s (% of peak), B=256 x 151936 fp32 logits"
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def time_cpu_baseline(w, budget_s: float, max_rows: int):
+    """The torch-CPU restatement of the reference chain, row by row, as the
+    reference scheduler calls sample() (mini_engine/scheduler.py:268-275)."""
+    import torch
+
+    from oracle.torch_chain import cpu_ref
+
+    class P:  # the SamplingParams fields the chain reads
+        pass
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    rows = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < budget_s and rows < max_rows:
+        r = rows % w.B
+        p = P()
+        p.temperature = float(w.temperature[r])
+        p.top_k = int(w.top_k[r])
+        p.top_p = float(w.top_p[r])
+        p.repetition_penalty = float(w.penalty[r])
+        hist = w.hist_ids[w.hist_offsets[r]:w.hist_offsets[r + 1]].tolist()
+        g = torch.Generator().manual_seed(r)
+        cpu_ref(torch.from_numpy(w.logits[r]), p, hist, g)
+        rows += 1
+    dt = time.perf_counter() - t0
+    return {
+        "value": rows / dt, "unit": "rows/s", "cores": torch.get_num_threads(), "kind": "port",
+        "sample": (f"{rows} rows of the same workload through oracle/torch_chain.cpu_ref "
+                   f"(torch {torch.__version__} CPU ops in the order of mini_engine/sampling.py:36-69, "
+                   f"one row per call) in {dt:.1f} s; host {cpu_model()}, "
+                   f"capability {torch.backends.cpu.get_cpu_capability()}"),
+    }
+
+
+def load_traffic(workload: str):
+    """HBM bytes per launch from the committed rocprofv3 counter summary."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{workload}.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="zipf",
+                    choices=["zipf", "greedy", "peaked", "single", "flat16"])
+    ap.add_argument("--batch", type=int, default=None, help="override the workload's batch")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-parity", action="store_true")
+    ap.add_argument("--cold", action="store_true", help="also time with the MALL flushed")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported "
+              "(rows are independent: each GPU of a data-parallel deployment runs this "
+              "same launch on its own share of the batch)", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from mi355x_sampler import Sampler
+    from mi355x_sampler.workloads import make_workload
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    log(f"[bench] building workload {args.workload}")
+    w = make_workload(args.workload, B=args.batch)
+    d = w.to_device(dev)
+    s = Sampler(w.B, w.V, dev)
+    run = lambda: s.run(**d)
+
+    log(f"[bench] warmup {args.warmup}")
+    for _ in range(args.warmup):
+        run()
+    torch.cuda.synchronize()
+
+    # wall clock over exactly K steps
+    log(f"[bench] timed {args.steps} steps")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        run()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = 1e3 * wall / args.steps
+
+    # per-launch kernel durations from HIP events on the launch stream
+    stream = torch.cuda.current_stream(dev)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    for a, b in evs:
+        a.record(stream)
+        run()
+        b.record(stream)
+    torch.cuda.synchronize()
+    dur_us = np.array([a.elapsed_time(b) * 1e3 for a, b in evs])
+
+    cold = None
+    if args.cold:
+        flush = torch.empty(1 << 29, dtype=torch.uint8, device=dev)   # 512 MiB > 256 MiB MALL
+        cd = []
+        for _ in range(min(args.steps, 50)):
+            flush.add_(1)
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            run()
+            b.record(stream)
+            torch.cuda.synchronize()
+            cd.append(a.elapsed_time(b) * 1e3)
+        cd = np.array(cd)
+        cold = {"kernel_us_median": float(np.median(cd)),
+                "hbm_gbps": w.algorithmic_bytes() / (np.median(cd) * 1e-6) / 1e9}
+        del flush
+
+    parity = None
+    if not args.no_parity:
+        from oracle import oracle as orc
+        ref = orc.sample_rows(w.logits, w.temperature, w.top_k, w.top_p, w.penalty,
+                              w.hist_offsets, w.hist_ids, w.uniforms)
+        got = s.tokens.cpu().numpy()
+        st = s.status.cpu().numpy()
+        parity = {"rows": int(w.B), "token_match": bool(np.array_equal(got, ref.tokens)),
+                  "status_match": bool(np.array_equal(st, ref.status))}
+
+    algo = w.algorithmic_bytes()
+    mean_us = float(dur_us.mean())
+    achieved = algo / (mean_us * 1e-6) / 1e9
+    rows_per_s = w.B / (ms_per_step * 1e-3)
+    dtype = "fp16->fp32" if w.logits.dtype == np.float16 else "fp32"
+    traffic = load_traffic(args.workload) if args.batch is None else None
+    out = {
+        "metric": METRIC,
+        "value": rows_per_s,
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dtype,
+        "data": "synthetic (seeded numpy PCG64 rows; no model weights involved)",
+        "config": {
+            "workload": {
+                "zipf": "B=256 x V=151936 fp32 Zipf rows, per-row T~U[0.3,1.5], top_k~U{0..1000}, "
+                        "top_p~U[0.5,1), penalty~U[1,1.3] over 1024-id histories",
+                "greedy": "B=256 x V=151936 fp32 3*N(0,1), greedy argmax",
+                "peaked": "B=64 x V=151936 fp32 N(0,1)+12 at 5 ids, T=0.7 k=50 p=0.9 pen=1.1, 512-id histories",
+                "single": "B=1 x V=151936 fp32 3*N(0,1), T=0.8 k=50 p=0.9 pen=1.1, 64-id history",
+                "flat16": "B=1024 x V=151936 fp16 N(0,1), T=0.7 k=0 p=0.95 pen=1.05, 2048-id histories",
+            }[args.workload] if args.batch is None else f"{args.workload} with B={w.B}",
+            "B": int(w.B), "V": int(w.V),
+        },
+        "hbm_gbps": achieved,
+        "pct_of_hbm_peak": 100.0 * achieved / HBM_PEAK_GBPS,
+        "kernel_us": {"mean": mean_us, "median": float(np.median(dur_us)),
+                      "p10": float(np.percentile(dur_us, 10)), "p90": float(np.percentile(dur_us, 90))},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
+                     "algorithmic_bytes_per_launch": algo,
+                     "kernel": "k_sample (one launch per batch)"},
+        "cold_mall": cold,
+        "parity_vs_oracle": parity,
+    }
+    if not args.no_cpu:
+        log(f"[bench] cpu baseline ({args.cpu_seconds:.0f} s budget)")
+        out["cpu_baseline"] = time_cpu_baseline(w, args.cpu_seconds, max_rows=10 * w.B)
+    else:
+        out["cpu_baseline"] = None
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

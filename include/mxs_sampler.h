@@ -6,8 +6,8 @@
  *   -> softmax -> draw,
  * the chain of mini_engine/sampling.py:30-69, with per-row parameters passed
  * as device arrays.  Plain pointers and sizes only; every buffer belongs to
- * the caller and the library allocates nothing.  Calls are asynchronous and
- * ordered on `stream`.  Two calls may run concurrently only with distinct
+ * the caller and the library allocates nothing.  A call enqueues two kernels
+ * on `stream` and returns; two calls may run concurrently only with distinct
  * workspaces.
  *
  * Results per row (token ids, post-filter probabilities) are defined by the
@@ -64,23 +64,13 @@ const char* mxs_version(void);
 const char* mxs_status_string(int status);
 
 /*
- * Workspace size in bytes for a batch of B rows of V logits.  The workspace
- * starts with a control area of mxs_control_bytes(B) bytes (per-row arrival
- * counters) followed by the rows' top-k candidate lists.  It must be 256-byte
- * aligned.  The control area must be zero when mxs_sample starts, and every
- * call leaves it zero again, so consecutive calls with the same B need no
- * re-initialization.  A call with a different B writes candidates where the
- * other B's control area lies: zero the control area (mxs_workspace_init with
- * bytes = mxs_control_bytes(B)) before the first call and whenever B changes.
+ * Workspace size in bytes for a batch of B rows of V logits: per-(row, chunk)
+ * partial results and top-k candidate lists written by the first kernel and
+ * read by the second within the same call.  It must be 256-byte aligned; it
+ * needs no initialization and its contents need not survive between calls.
+ * Returns 0 for an invalid shape.
  */
 size_t mxs_workspace_bytes(int B, int V);
-
-/* Size of the control area at the start of the workspace for B rows. */
-size_t mxs_control_bytes(int B);
-
-/* Zero the first `bytes` bytes of a workspace on `stream` (a fill kernel, so
- * no memset node is recorded if the caller captures the stream). */
-int mxs_workspace_init(void* workspace, size_t bytes, mxs_stream_t stream);
 
 /*
  * Sample one token per row.  Replaces the per-row Python call

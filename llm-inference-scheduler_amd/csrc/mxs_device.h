@@ -19,18 +19,27 @@ constexpr int NT = 512;                 // threads per workgroup
 constexpr int NWAVES = NT / 64;
 constexpr int CS_MAX = 16384;           // logits staged in LDS per chunk
 constexpr int CS_MIN = 2048;
+constexpr int NC_MAX = 255;             // chunks per row
 constexpr int KMAX = 1024;              // largest top_k served by the candidate path
 constexpr int CHUNK_CAP = 2048;         // candidates one chunk may emit
+constexpr int CAND_LDS = 16384;         // candidate keys the finisher keeps in LDS
 constexpr int SORT_CAP = 4096;          // top-k survivors sorted in LDS (= 8 per thread)
-constexpr int LCAP = 2048;              // elements collected per refinement step (= 4 per thread)
+constexpr int LCAP = 4096;              // elements collected per refinement step (= 8 per thread)
 constexpr int MASS_SHIFT = 20;          // masses carry 44 fractional bits: 24-bit P << (20 + n)
 constexpr uint32_t SK_MIN = 0x007FFFFFu;  // selection key of -inf (T > 0) or +inf (T < 0)
 
-// LDS map of the sampling kernel (dynamic shared memory).
-constexpr int LDS_REGION = 65536;       // chunk logits / sort buffers / row bitmap
-constexpr int LDS_HIST = LDS_REGION;    // 2048 x u32 radix histogram
-constexpr int LDS_BM = LDS_HIST + 8192; // 512 x u32 chunk penalty bitmap
-constexpr int LDS_BYTES = LDS_BM + 2048;
+// LDS map of the chunk kernel (dynamic shared memory).
+constexpr int K1_XS = 0;                        // CS_MAX fp32 logits
+constexpr int K1_HIST = K1_XS + 4 * CS_MAX;     // 2048 x u32 radix histogram
+constexpr int K1_BM = K1_HIST + 8192;           // CS_MAX bits of penalty bitmap
+constexpr int K1_LDS_BYTES = K1_BM + CS_MAX / 8;
+
+// LDS map of the row kernel.
+constexpr int K2_A = 0;                         // 64 KB: candidate keys / row penalty bitmap
+constexpr int K2_B = 65536;                     // 64 KB: sort keys + prefix masses / histograms
+constexpr int K2_HIST = K2_B + 65536;           // 2048 x u32
+constexpr int K2_OFF = K2_HIST + 8192;          // NC_MAX + 1 candidate offsets
+constexpr int K2_LDS_BYTES = K2_OFF + 4 * (NC_MAX + 1);
 
 __host__ __device__ __forceinline__ uint32_t f2u(float f) { return __builtin_bit_cast(uint32_t, f); }
 __host__ __device__ __forceinline__ float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
@@ -139,6 +148,23 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
     return v;
 }
 
+template <typename T>
+__device__ __forceinline__ T block_max(T v)
+{
+    __shared__ T s[NWAVES];
+    for (int o = 32; o > 0; o >>= 1) {
+        T w = __shfl_xor(v, o, 64);
+        v = w > v ? w : v;
+    }
+    __syncthreads();
+    if (lane_id() == 0) s[wave_id()] = v;
+    __syncthreads();
+    T t = s[0];
+#pragma unroll
+    for (int i = 1; i < NWAVES; ++i) t = s[i] > t ? s[i] : t;
+    return t;
+}
+
 // Number of set bits of `mask` below this lane.
 __device__ __forceinline__ uint32_t lanes_below(u64 mask)
 {
@@ -213,13 +239,14 @@ __device__ BinHit find_desc(const T* h, int nb, u64 t)
     return r;
 }
 
-// kk-th largest (1-based) 32-bit key among key(i), i in [0, n), by an MSD radix
-// select with digits of 11, 11 and 10 bits and a 2048-entry LDS histogram.
-// When the bin holding the answer has at most `small` keys the search stops
-// and returns that bin's lower edge (a valid lower bound); small = 0 gives the
-// exact key.
-template <class KeyF>
-__device__ uint32_t block_select_desc(int n, uint32_t kk, KeyF key, uint32_t* hist, uint32_t small)
+// kk-th largest (1-based) 32-bit key among the keys a workgroup enumerates,
+// by an MSD radix select with digits of 11, 11 and 10 bits and a 2048-entry
+// LDS histogram.  `visit(f)` must call f(key) once for every key owned by the
+// calling thread (together the threads cover the whole set).  When the bin
+// holding the answer has at most `small` keys the search stops and returns
+// that bin's lower edge (a valid lower bound); small = 0 gives the exact key.
+template <class Visit>
+__device__ uint32_t block_select_desc_v(uint32_t kk, Visit visit, uint32_t* hist, uint32_t small)
 {
     const int shifts[3] = {21, 10, 0};
     const int widths[3] = {11, 11, 10};
@@ -229,10 +256,9 @@ __device__ uint32_t block_select_desc(int n, uint32_t kk, KeyF key, uint32_t* hi
         const int hsh = sh + widths[lev];
         for (int b = threadIdx.x; b < nb; b += NT) hist[b] = 0;
         __syncthreads();
-        for (int i = threadIdx.x; i < n; i += NT) {
-            uint32_t k = key(i);
+        visit([&](uint32_t k) {
             if (lev == 0 || (k >> hsh) == prefix) atomicAdd(&hist[(k >> sh) & (nb - 1)], 1u);
-        }
+        });
         __syncthreads();
         BinHit hit = find_desc<uint32_t>(hist, nb, (u64)(kk - 1));
         kk -= (uint32_t)hit.above;
@@ -242,6 +268,15 @@ __device__ uint32_t block_select_desc(int n, uint32_t kk, KeyF key, uint32_t* hi
         if (cnt <= small || lev == 2) return prefix << sh;
     }
     return prefix;
+}
+
+// Indexed form: keys key(i) for i in [0, n).
+template <class KeyF>
+__device__ uint32_t block_select_desc(int n, uint32_t kk, KeyF key, uint32_t* hist, uint32_t small)
+{
+    return block_select_desc_v(kk, [&](auto&& f) {
+        for (int i = threadIdx.x; i < n; i += NT) f(key(i));
+    }, hist, small);
 }
 
 // Bitonic sort of P (power of two) u64 keys in LDS, descending.

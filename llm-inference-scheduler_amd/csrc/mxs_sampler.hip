@@ -1,26 +1,26 @@
 // mxs_sampler.hip -- gfx950 sampler chain behind the C ABI of include/mxs_sampler.h.
 //
-// One kernel launch samples a whole [B, V] batch.  The grid is B x NC
-// workgroups; workgroup (r, c) owns chunk c of row r (<= 16384 logits):
+// Reference chain: mini_engine/sampling.py:30-69, one [vocab] row per call.
+// Here one call samples a whole [B, V] batch with two launches:
 //
-//   1. stream the chunk from HBM once in 128-bit loads into LDS (fp16 rows are
-//      upcast to fp32 there), apply the repetition penalty in place for the
-//      history ids that fall in the chunk (LDS bitmap: each id once);
-//   2. per row mode:
-//        greedy  - chunk argmax, packed (key, ~index) -> 64-bit atomicMax
-//        top-k   - MSD radix select on order-preserving keys (LDS histogram)
-//                  for the chunk's k-th largest, widened by the rounding of
-//                  x / T, and the chunk's survivors appended to the row's
-//                  candidate list
-//        other   - chunk max only
-//   3. the last workgroup of the row to arrive (device-scope counter, no
-//      waiting) finishes the row: exact top-k over the candidates, bitonic
-//      sort in LDS, integer softmax masses, exact top-p cut, inverse-CDF draw.
-//      Rows with top-k off or larger than KMAX take a multi-pass path over the
-//      row in the same workgroup (mass histograms, then collecting the one
-//      histogram bin that holds the answer).
-//
-// Reference chain: mini_engine/sampling.py:30-69.
+// k_chunks  grid B x NC, workgroup (r, c) owns chunk c of row r (<= 16384
+//           logits).  It streams the chunk from HBM once in 128-bit loads into
+//           LDS (fp16 upcast to fp32 there), applies the repetition penalty in
+//           place for the history ids inside the chunk (an LDS bitmap marks
+//           each id once), then per row mode:
+//             greedy  chunk argmax as a packed (key, ~index)
+//             top-k   MSD radix select on order-preserving keys for the
+//                     chunk's k-th largest, widened over the rounding of x / T,
+//                     and the survivors written to the chunk's candidate slot
+//             other   chunk maximum only
+//           Results go to fixed per-(row, chunk) slots: no atomics, no
+//           cross-workgroup waits, nothing to clear between calls.
+// k_rows    grid B, one workgroup per row, after k_chunks (the kernel boundary
+//           makes the slots visible).  Exact top-k over the candidates, bitonic
+//           sort in LDS, integer softmax masses, exact top-p cut, inverse-CDF
+//           draw.  Rows with top-k off or above KMAX (or whose candidates
+//           overflow) are resolved by multi-pass histogram refinement over the
+//           row in global memory.
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 #include <stddef.h>
@@ -33,14 +33,12 @@ using namespace mxs;
 
 namespace {
 
-struct RowCtl {            // 32 bytes per row, all zero between calls
-    u64 best;              // greedy: max (key << 32 | ~index); others: max selection key << 32
-    uint32_t arrive;       // chunks done
-    uint32_t ncand;        // candidates appended
+struct ChunkOut {          // one slot per (row, chunk), 16 bytes
+    u64 best;              // greedy: max (key << 32 | ~index); sampling rows: max selection key << 32
+    uint32_t count;        // candidates written to the chunk's slot
     uint32_t flags;
-    uint32_t pad[3];
 };
-static_assert(sizeof(RowCtl) == 32, "RowCtl layout");
+static_assert(sizeof(ChunkOut) == 16, "ChunkOut layout");
 
 enum : uint32_t { FLAG_BAD_HISTORY = 1u, FLAG_OVERFLOW = 2u };
 enum RowMode { MODE_GREEDY = 0, MODE_TOPK = 1, MODE_LARGE = 2, MODE_INVALID = 3 };
@@ -49,7 +47,7 @@ struct Params {
     const void* logits;
     int B, V;
     long long ld;
-    int CS, NC, capr;
+    int CS, NC;
     const float* T;
     const int32_t* K;
     const float* P;
@@ -60,12 +58,13 @@ struct Params {
     int64_t* out_tok;
     int32_t* out_status;
     float* out_probs;
-    RowCtl* ctl;
-    u64* cand;
+    ChunkOut* parts;       // [B * NC]
+    uint32_t* cand_sk;     // [B * NC * CHUNK_CAP] selection keys
+    uint32_t* cand_idx;    // [B * NC * CHUNK_CAP] token ids
 };
 
 struct Geometry {
-    int NC, CS, capr;
+    int NC, CS;
 };
 
 Geometry geometry(int B, int V)
@@ -74,15 +73,14 @@ Geometry geometry(int B, int V)
     auto cdiv = [](long long a, long long b) { return (int)((a + b - 1) / b); };
     int nc_min = cdiv(V, CS_MAX);
     int nc_max = cdiv(V, CS_MIN);
+    if (nc_max > NC_MAX) nc_max = NC_MAX;
     int want = cdiv(target_wgs, B > 0 ? B : 1);
     int NC = want < nc_max ? want : nc_max;
     if (NC < nc_min) NC = nc_min;
     if (NC < 1) NC = 1;
     int CS = cdiv(cdiv(V, NC), 8) * 8;
     NC = cdiv(V, CS);
-    long long capr = (long long)NC * CHUNK_CAP;
-    if (capr > V) capr = V;
-    return Geometry{NC, CS, (int)capr};
+    return Geometry{NC, CS};
 }
 
 __device__ __forceinline__ RowMode classify(float T, int k, int V)
@@ -125,10 +123,10 @@ template <> struct VecIO<__half> {
 
 __device__ __forceinline__ float penalize(float v, float pen) { return v > 0.0f ? v / pen : v * pen; }
 
-// Largest-first search for the smallest selection key s whose tempered value
-// fl32(x(s) / T) is >= fl32(x(th) / T).  Division by T is monotone, so the
-// predicate is monotone in s; values within a few ulps of x(th) can round onto
-// the same tempered value and must join the candidate set.
+// The smallest selection key s whose tempered value fl32(x(s) / T) is
+// >= fl32(x(th) / T).  Division by T is monotone, so the predicate is
+// monotone in s; values a few ulps below x(th) can round onto the same
+// tempered value and then tie with it.
 __device__ uint32_t widen_threshold(uint32_t th, float T, bool neg)
 {
     __shared__ uint32_t s_res;
@@ -162,6 +160,160 @@ __device__ uint32_t widen_threshold(uint32_t th, float T, bool neg)
     return r;
 }
 
+// ================================================================ k_chunks
+
+template <typename TIn>
+__global__ __launch_bounds__(NT, 2) void k_chunks(Params p)
+{
+    extern __shared__ __align__(16) unsigned char smem[];
+    float* xs = (float*)(smem + K1_XS);
+    uint32_t* hist = (uint32_t*)(smem + K1_HIST);
+    uint32_t* bm = (uint32_t*)(smem + K1_BM);
+    __shared__ uint32_t s_wcnt;
+
+    const int tid = threadIdx.x;
+    const int r = blockIdx.x / p.NC;
+    const int c = blockIdx.x - r * p.NC;
+    const int V = p.V;
+    const float T = p.T[r];
+    const int k = p.K[r];
+    const float pen = p.PEN[r];
+    const RowMode mode = classify(T, k, V);
+    const bool neg = T < 0.0f;
+    const int e0 = c * p.CS;
+    const int e1 = (e0 + p.CS < V) ? e0 + p.CS : V;
+    const int n = e1 - e0;
+    const TIn* rowp = (const TIn*)p.logits + (size_t)r * (size_t)p.ld;
+    const int h0 = p.hoff ? p.hoff[r] : 0;
+    const int h1 = p.hoff ? p.hoff[r + 1] : 0;
+    const bool pen_on = (pen != 1.0f) && (h1 > h0);
+    const size_t slot = (size_t)blockIdx.x;
+
+    if (p.out_probs) {
+        float* o = p.out_probs + (size_t)r * (size_t)V;
+        for (int i = e0 + tid; i < e1; i += NT) o[i] = 0.0f;
+    }
+
+    // ---- stream the chunk into LDS; penalty bitmap from the history
+    typedef VecIO<TIn> IO;
+    constexpr int VW = IO::W;
+    constexpr int MAXV = CS_MAX / (NT * VW);
+    if (pen_on)
+        for (int w = tid; w < CS_MAX / 32; w += NT) bm[w] = 0;
+    __syncthreads();
+    // 128-bit loads when the chunk start is 16-byte aligned (every chunk of a
+    // row whose start is: CS is a multiple of 8 elements), scalar otherwise.
+    const bool vec_ok = (((uintptr_t)(rowp + e0)) & 15u) == 0;
+    const int nvec = vec_ok ? n / VW : 0;
+    typename IO::vec_t regs[MAXV];
+    const typename IO::vec_t* src = (const typename IO::vec_t*)(rowp + e0);
+#pragma unroll
+    for (int j = 0; j < MAXV; ++j) {
+        int v = tid + j * NT;
+        regs[j] = typename IO::vec_t{};
+        if (v < nvec) regs[j] = src[v];
+    }
+    uint32_t flags = 0;
+    if (pen_on) {
+        bool bad = false;
+        for (int h = h0 + tid; h < h1; h += NT) {
+            int id = p.hids[h];
+            if (id < 0 || id >= V) { bad = true; continue; }
+            if (id >= e0 && id < e1) {
+                int o = id - e0;
+                atomicOr(&bm[o >> 5], 1u << (o & 31));
+            }
+        }
+        if (block_sum<uint32_t>(bad ? 1u : 0u)) flags |= FLAG_BAD_HISTORY;
+    }
+#pragma unroll
+    for (int j = 0; j < MAXV; ++j) {
+        int v = tid + j * NT;
+        if (v < nvec) IO::put(xs + v * VW, regs[j]);
+    }
+    for (int i = nvec * VW + tid; i < n; i += NT) xs[i] = IO::one(rowp, e0 + i);
+    __syncthreads();
+    if (pen_on) {   // sampling.py:38-45, each id once
+        for (int w = tid; w < (n + 31) / 32; w += NT) {
+            uint32_t bits = bm[w];
+            while (bits) {
+                int b = __builtin_ctz(bits);
+                bits &= bits - 1u;
+                int o = w * 32 + b;
+                xs[o] = penalize(xs[o], pen);
+            }
+        }
+        __syncthreads();
+    }
+
+    // ---- per-mode chunk work
+    u64 best = 0;
+    uint32_t count = 0;
+    if (mode == MODE_GREEDY) {   // sampling.py:47-48
+        u64 b = 0;
+        for (int i = tid; i < n; i += NT) {
+            float x = xs[i];
+            uint32_t g = (x != x) ? 0xFFFFFFFFu : vkey(x);
+            u64 v = ((u64)g << 32) | (u64)(0xFFFFFFFFu - (uint32_t)(e0 + i));
+            b = v > b ? v : b;
+        }
+        best = block_max<u64>(b);
+    } else if (mode == MODE_TOPK || mode == MODE_LARGE) {
+        uint32_t mx = 0;
+        for (int i = tid; i < n; i += NT) {
+            uint32_t s = selkey(xs[i], neg);
+            mx = s > mx ? s : mx;
+        }
+        best = (u64)block_max<uint32_t>(mx) << 32;
+
+        if (mode == MODE_TOPK) {   // sampling.py:52-54, a superset of the chunk's share
+            uint32_t theta = 0;
+            if (n > k) {
+                auto key = [&](int i) -> uint32_t { return selkey(xs[i], neg); };
+                uint32_t th = block_select_desc(n, (uint32_t)k, key, hist, 32u);
+                if (th < SK_MIN) th = SK_MIN;
+                theta = widen_threshold(th, T, neg);
+            }
+            uint32_t mine = 0;
+            for (int i = tid; i < n; i += NT) mine += selkey(xs[i], neg) >= theta ? 1u : 0u;
+            const uint32_t total = block_sum<uint32_t>(mine);
+            if (total > (uint32_t)CHUNK_CAP) {
+                flags |= FLAG_OVERFLOW;
+            } else {
+                count = total;
+                if (tid == 0) s_wcnt = 0;
+                __syncthreads();
+                uint32_t* dsk = p.cand_sk + slot * CHUNK_CAP;
+                uint32_t* didx = p.cand_idx + slot * CHUNK_CAP;
+                for (int i0 = 0; i0 < n; i0 += NT) {
+                    int i = i0 + tid;
+                    uint32_t s = 0;
+                    bool keep = false;
+                    if (i < n) {
+                        s = selkey(xs[i], neg);
+                        keep = s >= theta;
+                    }
+                    u64 mask = __ballot(keep);
+                    if (mask) {
+                        int first = __builtin_ctzll(mask);
+                        uint32_t wb = 0;
+                        if (lane_id() == first) wb = atomicAdd(&s_wcnt, (uint32_t)__builtin_popcountll(mask));
+                        wb = __shfl(wb, first, 64);
+                        if (keep) {
+                            uint32_t o = wb + lanes_below(mask);
+                            dsk[o] = s;
+                            didx[o] = (uint32_t)(e0 + i);
+                        }
+                    }
+                }
+            }
+        }
+    }
+    if (tid == 0) p.parts[slot] = ChunkOut{best, count, flags};
+}
+
+// ================================================================ k_rows
+
 struct Found {
     uint32_t vk;
     uint32_t idx;
@@ -169,12 +321,9 @@ struct Found {
     u64 w;     // the element's mass
 };
 
-// ------------------------------------------------------------------ large path
-//
-// Single-workgroup, multi-pass resolution of a row over its logits in global
-// memory: used when top-k is off or larger than KMAX, and when the candidate
-// path overflows (massive ties).  All passes read the row with the penalty
-// applied through a full-row LDS bitmap.
+// Multi-pass resolution of one row over its logits in global memory: used
+// when top-k is off or above KMAX, and when candidates overflow (massive ties).
+// Penalized values come from a full-row LDS bitmap of the history.
 template <typename TIn>
 struct LargeRow {
     const TIn* row;
@@ -184,12 +333,11 @@ struct LargeRow {
     float pen;
     bool pen_on;
     const uint32_t* rbm;   // V bits
-    uint32_t thk;          // kept-by-top-k: selection key >= thk
+    uint32_t thk;          // kept by top-k: selection key >= thk
     float m;               // max tempered logit
     u64* MH;               // 2048 masses (overlaps keys)
     uint32_t* CH;          // 2048 counts
     u64* keys;             // LCAP sort keys
-    u64* wm;               // LCAP masses / prefix sums
 
     __device__ float x_at(int i) const
     {
@@ -220,15 +368,13 @@ struct LargeRow {
             atomicAdd(&CH[d], 1u);
             tot += w;
         }
-        tot = block_sum<u64>(tot);
-        return tot;
+        return block_sum<u64>(tot);
     }
 
-    // q-th smallest index (0-based) among kept elements whose value key is vk.
+    // q-th smallest index (0-based) among the `count` kept elements whose value key is vk.
     __device__ uint32_t select_index(uint32_t vk, uint32_t q, uint32_t count)
     {
-        // digits of the index: [17:9] then [8:0] (V <= 2^18)
-        uint32_t* H = CH;
+        uint32_t* H = CH;   // digits of the index: [17:9] then [8:0] (V <= 2^18)
         uint32_t hi_bin = 0;
         for (int lev = 0; lev < 2; ++lev) {
             for (int b = threadIdx.x; b < 512; b += NT) H[b] = 0;
@@ -243,22 +389,20 @@ struct LargeRow {
             __syncthreads();
             // the q-th smallest is the (count - q)-th largest
             BinHit hit = find_desc<uint32_t>(H, 512, (u64)(count - 1u - q));
-            uint32_t below = count - (uint32_t)hit.above - H[hit.bin];
+            uint32_t in_bin = H[hit.bin];
+            uint32_t below = count - (uint32_t)hit.above - in_bin;
             __syncthreads();
-            if (lev == 0) {
-                hi_bin = (uint32_t)hit.bin;
-                count = count - (uint32_t)hit.above - below;   // members in this bin
-                q -= below;
-            } else {
-                return (hi_bin << 9) | (uint32_t)hit.bin;
-            }
+            if (lev == 1) return (hi_bin << 9) | (uint32_t)hit.bin;
+            hi_bin = (uint32_t)hit.bin;
+            count = in_bin;
+            q -= below;
         }
         return 0;
     }
 
-    // The element at mass position t (0 <= t < total kept-by-k mass) of the
-    // sorted order (value descending, index ascending).  If mh0_ready, the
-    // level-0 histogram is already in MH/CH.
+    // The element at mass position t (t < total kept mass) of the sorted order
+    // (value descending, index ascending).  If mh0_ready the level-0
+    // histogram is already in MH/CH.
     __device__ Found find(u64 t, bool mh0_ready)
     {
         __shared__ Found s_found;
@@ -284,8 +428,8 @@ struct LargeRow {
                     if (selkey(x, neg) < thk) continue;
                     uint32_t vk = vkey(x / T);
                     if ((vk >> sh) != key_prefix) continue;
-                    uint32_t slot = atomicAdd(&s_cnt, 1u);
-                    if (slot < (uint32_t)LCAP) keys[slot] = ((u64)vk << 32) | (u64)(0xFFFFFFFFu - (uint32_t)i);
+                    uint32_t o = atomicAdd(&s_cnt, 1u);
+                    if (o < (uint32_t)LCAP) keys[o] = ((u64)vk << 32) | (u64)(0xFFFFFFFFu - (uint32_t)i);
                 }
                 __syncthreads();
                 const int n = (int)cnt;
@@ -293,26 +437,25 @@ struct LargeRow {
                 for (int j = n + threadIdx.x; j < P; j += NT) keys[j] = 0;
                 __syncthreads();
                 bitonic_sort_desc(keys, P);
-                // prefix masses, 4 consecutive per thread
-                const int j0 = threadIdx.x * 4;
-                u64 w4[4], run = 0;
-                for (int q = 0; q < 4; ++q) {
+                constexpr int PER = LCAP / NT;
+                const int j0 = threadIdx.x * PER;
+                u64 wv[PER], run = 0;
+#pragma unroll
+                for (int q = 0; q < PER; ++q) {
                     int j = j0 + q;
                     u64 w = 0;
                     if (j < n) w = mass_of(okey_inv((uint32_t)(keys[j] >> 32)) - m);
-                    w4[q] = w;
+                    wv[q] = w;
                     run += w;
                 }
                 u64 tot;
-                u64 excl = block_incl_scan<u64>(run, &tot) - run;
-                u64 E = A_b + excl;
-                for (int q = 0; q < 4; ++q) {
+                u64 E = A_b + (block_incl_scan<u64>(run, &tot) - run);
+#pragma unroll
+                for (int q = 0; q < PER; ++q) {
                     int j = j0 + q;
-                    if (j < n && E <= t && t < E + w4[q]) {
-                        uint32_t idx = 0xFFFFFFFFu - (uint32_t)keys[j];
-                        s_found = Found{(uint32_t)(keys[j] >> 32), idx, E, w4[q]};
-                    }
-                    E += w4[q];
+                    if (j < n && E <= t && t < E + wv[q])
+                        s_found = Found{(uint32_t)(keys[j] >> 32), 0xFFFFFFFFu - (uint32_t)keys[j], E, wv[q]};
+                    E += wv[q];
                 }
                 __syncthreads();
                 Found f = s_found;
@@ -324,7 +467,7 @@ struct LargeRow {
                 prefix = key_prefix;
                 continue;
             }
-            // one value shared by more than LCAP elements: equal masses, order by index
+            // one value shared by more than LCAP elements: equal masses, index order
             const u64 w = mass_b / cnt;
             const u64 q = (t - A_b) / w;
             uint32_t idx = select_index(key_prefix, (uint32_t)q, cnt);
@@ -339,7 +482,6 @@ __device__ void finish_large(const Params& p, int r, float T, int k, float top_p
                              bool pen_on, u64 best, float u, int64_t& tok, int32_t& st)
 {
     extern __shared__ __align__(16) unsigned char smem[];
-    unsigned char* smem_base = smem;
     const int V = p.V;
     LargeRow<TIn> L;
     L.row = (const TIn*)p.logits + (size_t)r * (size_t)p.ld;
@@ -348,31 +490,28 @@ __device__ void finish_large(const Params& p, int r, float T, int k, float top_p
     L.neg = T < 0.0f;
     L.pen = pen;
     L.pen_on = pen_on;
-    uint32_t* rbm = (uint32_t*)smem_base;                 // [0, 32K)
+    uint32_t* rbm = (uint32_t*)(smem + K2_A);
     L.rbm = rbm;
-    L.MH = (u64*)(smem_base + 32768);                      // [32K, 48K)
-    L.keys = (u64*)(smem_base + 32768);
-    L.wm = (u64*)(smem_base + 49152);                      // [48K, 64K)
-    L.CH = (uint32_t*)(smem_base + LDS_HIST);
+    L.MH = (u64*)(smem + K2_B);
+    L.keys = (u64*)(smem + K2_B);
+    L.CH = (uint32_t*)(smem + K2_HIST);
 
     if (pen_on) {
         const int words = (V + 31) >> 5;
         for (int w = threadIdx.x; w < words; w += NT) rbm[w] = 0;
         __syncthreads();
-        const int h0 = p.hoff[r], h1 = p.hoff[r + 1];
-        for (int h = h0 + threadIdx.x; h < h1; h += NT) {
-            int id = p.hids[h];
-            atomicOr(&rbm[id >> 5], 1u << (id & 31));     // ids validated by the chunks
+        for (int h = p.hoff[r] + threadIdx.x; h < p.hoff[r + 1]; h += NT) {
+            int id = p.hids[h];     // range-checked by k_chunks
+            atomicOr(&rbm[id >> 5], 1u << (id & 31));
         }
         __syncthreads();
     }
 
-    const float xmax = sel_inv((uint32_t)(best >> 32), L.neg);
-    const float m = xmax / T;
+    const float m = sel_inv((uint32_t)(best >> 32), L.neg) / T;
     if (!isfinite(m)) { st = MXS_ROW_NONFINITE; tok = -1; return; }
     L.m = m;
 
-    // sampling.py:52-54 -- exact k-th largest over the whole row
+    // sampling.py:52-54: exact k-th largest over the row
     L.thk = 0;
     if (k > 0 && k < V) {
         auto key = [&](int i) -> uint32_t { return selkey(L.x_at(i), L.neg); };
@@ -382,84 +521,110 @@ __device__ void finish_large(const Params& p, int r, float T, int k, float top_p
     }
 
     // sampling.py:56-66 and 69
-    u64 W = L.mass_hist(0, 0);
+    const u64 W = L.mass_hist(0, 0);
     bool have_bound = false;
     uint32_t vk_b = 0, idx_b = 0;
     u64 Wk = W;
     bool mh0 = true;
     if (top_p < 1.0f) {
         if (!(top_p > 0.0f)) { st = MXS_ROW_EMPTY_NUCLEUS; tok = -1; return; }
-        u64 Tm = ceil_mul(top_p, W);
-        Found b = L.find(Tm - 1, true);
+        Found b = L.find(ceil_mul(top_p, W) - 1, true);
         have_bound = true;
         vk_b = b.vk;
         idx_b = b.idx;
         Wk = b.E + b.w;
         mh0 = false;
     }
-    u64 D = floor_mul(clamp_uniform(u), Wk);
-    Found d = L.find(D, mh0);
+    Found d = L.find(floor_mul(clamp_uniform(u), Wk), mh0);
     tok = (int64_t)d.idx;
     st = MXS_ROW_OK;
 
     // sampling.py:68
     if (p.out_probs) {
         float* out = p.out_probs + (size_t)r * (size_t)V;
-        const double inv = (double)Wk;
         for (int i = threadIdx.x; i < V; i += NT) {
             float x = L.x_at(i);
             if (selkey(x, L.neg) < L.thk) continue;
             float l = x / T;
             uint32_t vk = vkey(l);
             if (have_bound && !(vk > vk_b || (vk == vk_b && (uint32_t)i <= idx_b))) continue;
-            out[i] = (float)((double)mass_of(l - m) / inv);
+            out[i] = (float)((double)mass_of(l - m) / (double)Wk);
         }
     }
 }
 
-// Top-k rows: candidates from every chunk are a superset of the row's top-k
-// survivors.  Returns false when the survivors do not fit the LDS sort, in
-// which case the caller resolves the row on the large path.
+// Top-k rows.  The chunks' candidates hold every element whose tempered
+// value reaches the row's k-th largest.  Returns false when the survivors do
+// not fit the LDS sort; the caller then takes the multi-pass path.
 __device__ bool finish_topk(const Params& p, int r, float T, int k, float top_p, float u,
-                            uint32_t ncand, int64_t& tok, int32_t& st)
+                            const uint32_t* counts, const uint32_t* off, int N,
+                            int64_t& tok, int32_t& st)
 {
     extern __shared__ __align__(16) unsigned char smem[];
-    u64* keys = (u64*)smem;                   // SORT_CAP keys  [0, 32K)
-    u64* cum = (u64*)(smem + 32768);          // SORT_CAP prefix masses [32K, 64K)
-    uint32_t* hist = (uint32_t*)(smem + LDS_HIST);
+    uint32_t* ck = (uint32_t*)(smem + K2_A);          // CAND_LDS candidate keys
+    u64* keys = (u64*)(smem + K2_B);                  // SORT_CAP sort keys
+    u64* cum = (u64*)(smem + K2_B + 8 * SORT_CAP);    // SORT_CAP prefix masses
+    uint32_t* hist = (uint32_t*)(smem + K2_HIST);
     __shared__ uint32_t s_n;
-    const u64* cand = p.cand + (size_t)r * (size_t)p.capr;
-    const int N = (int)ncand;
-    const int V = p.V;
+    const int NC = p.NC, V = p.V;
+    const bool neg = T < 0.0f;
     const uint32_t kk = (uint32_t)(k < V ? k : V);
+    const size_t slot0 = (size_t)r * NC;
+    const bool in_lds = N <= CAND_LDS;
 
-    auto lkey = [&](int i) -> uint32_t { return vkey(u2f((uint32_t)(cand[i] >> 32)) / T); };
-    const uint32_t vk_kth = block_select_desc(N, kk, lkey, hist, 0u);
+    if (in_lds) {
+        for (int c = 0; c < NC; ++c) {
+            const uint32_t* src = p.cand_sk + (slot0 + c) * CHUNK_CAP;
+            for (int j = threadIdx.x; j < (int)counts[c]; j += NT) ck[off[c] + j] = src[j];
+        }
+        __syncthreads();
+    }
+    auto visit = [&](auto&& f) {
+        if (in_lds) {
+            for (int i = threadIdx.x; i < N; i += NT) f(ck[i]);
+        } else {
+            for (int c = 0; c < NC; ++c) {
+                const uint32_t* src = p.cand_sk + (slot0 + c) * CHUNK_CAP;
+                for (int j = threadIdx.x; j < (int)counts[c]; j += NT) f(src[j]);
+            }
+        }
+    };
 
+    // sampling.py:52-54: the k-th largest, then everything that rounds onto it
+    uint32_t sk_k = block_select_desc_v(kk, visit, hist, 0u);
+    if (sk_k < SK_MIN) sk_k = SK_MIN;
+    const uint32_t theta = widen_threshold(sk_k, T, neg);
     uint32_t mine = 0;
-    for (int i = threadIdx.x; i < N; i += NT) mine += lkey(i) >= vk_kth ? 1u : 0u;
+    visit([&](uint32_t s) { mine += s >= theta ? 1u : 0u; });
     const int n1 = (int)block_sum<uint32_t>(mine);
     if (n1 > SORT_CAP) return false;
 
     if (threadIdx.x == 0) s_n = 0;
     __syncthreads();
-    for (int i0 = 0; i0 < N; i0 += NT) {
-        int i = i0 + threadIdx.x;
-        uint32_t vk = 0;
-        bool keep = false;
-        u64 e = 0;
-        if (i < N) {
-            e = cand[i];
-            vk = vkey(u2f((uint32_t)(e >> 32)) / T);
-            keep = vk >= vk_kth;
-        }
-        u64 mask = __ballot(keep);
-        if (mask) {
-            int first = __builtin_ctzll(mask);
-            uint32_t base = 0;
-            if (lane_id() == first) base = atomicAdd(&s_n, (uint32_t)__builtin_popcountll(mask));
-            base = __shfl(base, first, 64);
-            if (keep) keys[base + lanes_below(mask)] = ((u64)vk << 32) | (u64)(0xFFFFFFFFu - (uint32_t)e);
+    for (int c = 0; c < NC; ++c) {
+        const int cnt = (int)counts[c];
+        const uint32_t* gsk = p.cand_sk + (slot0 + c) * CHUNK_CAP;
+        const uint32_t* gidx = p.cand_idx + (slot0 + c) * CHUNK_CAP;
+        for (int j0 = 0; j0 < cnt; j0 += NT) {
+            const int j = j0 + threadIdx.x;
+            uint32_t s = 0;
+            bool keep = false;
+            if (j < cnt) {
+                s = in_lds ? ck[off[c] + j] : gsk[j];
+                keep = s >= theta;
+            }
+            u64 mask = __ballot(keep);
+            if (mask) {
+                int first = __builtin_ctzll(mask);
+                uint32_t base = 0;
+                if (lane_id() == first) base = atomicAdd(&s_n, (uint32_t)__builtin_popcountll(mask));
+                base = __shfl(base, first, 64);
+                if (keep) {
+                    const uint32_t idx = gidx[j];
+                    const uint32_t vk = vkey(sel_inv(s, neg) / T);
+                    keys[base + lanes_below(mask)] = ((u64)vk << 32) | (u64)(0xFFFFFFFFu - idx);
+                }
+            }
         }
     }
     __syncthreads();
@@ -468,25 +633,26 @@ __device__ bool finish_topk(const Params& p, int r, float T, int k, float top_p,
     __syncthreads();
     bitonic_sort_desc(keys, P);
 
-    // sampling.py:57-59: masses in sorted order, inclusive prefix sums
+    // sampling.py:57-59: masses in sorted order and their inclusive prefix sums
     const float m = okey_inv((uint32_t)(keys[0] >> 32));
     if (!isfinite(m)) { st = MXS_ROW_NONFINITE; tok = -1; return true; }
-    const int j0 = threadIdx.x * 8;
-    u64 w8[8], run = 0;
+    constexpr int PER = SORT_CAP / NT;
+    const int j0 = threadIdx.x * PER;
+    u64 wv[PER], run = 0;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
+    for (int q = 0; q < PER; ++q) {
         int j = j0 + q;
         u64 w = 0;
         if (j < n1) w = mass_of(okey_inv((uint32_t)(keys[j] >> 32)) - m);
-        w8[q] = w;
+        wv[q] = w;
         run += w;
     }
     u64 W;
-    u64 c = block_incl_scan<u64>(run, &W) - run;
+    u64 acc = block_incl_scan<u64>(run, &W) - run;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-        c += w8[q];
-        if (j0 + q < SORT_CAP) cum[j0 + q] = c;
+    for (int q = 0; q < PER; ++q) {
+        acc += wv[q];
+        cum[j0 + q] = acc;
     }
     __syncthreads();
 
@@ -497,19 +663,19 @@ __device__ bool finish_topk(const Params& p, int r, float T, int k, float top_p,
         const u64 Tm = ceil_mul(top_p, W);
         uint32_t cnt = 0;
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
+        for (int q = 0; q < PER; ++q) {
             int j = j0 + q;
-            if (j < n1 && cum[j] - w8[q] < Tm) ++cnt;
+            if (j < n1 && cum[j] - wv[q] < Tm) ++cnt;
         }
         nstar = (int)block_sum<uint32_t>(cnt);
     }
     const u64 Wk = cum[nstar - 1];
 
-    // sampling.py:69: first j with C_j > floor(u * Wk)
+    // sampling.py:69: the first j with C_j > floor(u * Wk)
     const u64 D = floor_mul(clamp_uniform(u), Wk);
     uint32_t below = 0;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
+    for (int q = 0; q < PER; ++q) {
         int j = j0 + q;
         if (j < nstar && cum[j] <= D) ++below;
     }
@@ -529,175 +695,44 @@ __device__ bool finish_topk(const Params& p, int r, float T, int k, float top_p,
 }
 
 template <typename TIn>
-__global__ __launch_bounds__(NT, 2) void k_sample(Params p)
+__global__ __launch_bounds__(NT, 1) void k_rows(Params p)
 {
     extern __shared__ __align__(16) unsigned char smem[];
-    float* xs = (float*)smem;
-    uint32_t* hist = (uint32_t*)(smem + LDS_HIST);
-    uint32_t* bm = (uint32_t*)(smem + LDS_BM);
-    __shared__ uint32_t s_base, s_wcnt, s_last;
-
+    uint32_t* off = (uint32_t*)(smem + K2_OFF);
+    __shared__ uint32_t s_counts[NC_MAX];
     const int tid = threadIdx.x;
-    const int r = blockIdx.x / p.NC;
-    const int c = blockIdx.x - r * p.NC;
-    const int V = p.V;
+    const int r = blockIdx.x;
+    const int NC = p.NC, V = p.V;
     const float T = p.T[r];
     const int k = p.K[r];
     const float pen = p.PEN[r];
     const RowMode mode = classify(T, k, V);
-    const bool neg = T < 0.0f;
-    const int e0 = c * p.CS;
-    const int e1 = (e0 + p.CS < V) ? e0 + p.CS : V;
-    const int n = e1 - e0;
-    RowCtl* ctl = p.ctl + r;
-    const TIn* rowp = (const TIn*)p.logits + (size_t)r * (size_t)p.ld;
     const int h0 = p.hoff ? p.hoff[r] : 0;
     const int h1 = p.hoff ? p.hoff[r + 1] : 0;
     const bool pen_on = (pen != 1.0f) && (h1 > h0);
 
-    if (p.out_probs) {
-        float* o = p.out_probs + (size_t)r * (size_t)V;
-        for (int i = e0 + tid; i < e1; i += NT) o[i] = 0.0f;
+    u64 best = 0;
+    uint32_t fl = 0;
+    for (int c = tid; c < NC; c += NT) {
+        ChunkOut o = p.parts[(size_t)r * NC + c];
+        best = o.best > best ? o.best : best;
+        fl |= o.flags;
+        s_counts[c] = o.count;
     }
-
-    // ---- 1. stream the chunk into LDS, penalty bitmap from the history
-    typedef VecIO<TIn> IO;
-    constexpr int VW = IO::W;
-    constexpr int MAXV = CS_MAX / (NT * VW);
-    if (pen_on) {
-        for (int w = tid; w < CS_MAX / 32; w += NT) bm[w] = 0;
+    best = block_max<u64>(best);
+    const uint32_t flags = block_max<uint32_t>(fl & FLAG_BAD_HISTORY) |
+                           block_max<uint32_t>(fl & FLAG_OVERFLOW);
+    if (tid == 0) {
+        uint32_t a = 0;
+        for (int c = 0; c < NC; ++c) { off[c] = a; a += s_counts[c]; }
+        off[NC] = a;
     }
     __syncthreads();
-    // 128-bit loads when the chunk start is 16-byte aligned (every chunk of a
-    // row whose start is: CS is a multiple of 8 elements), scalar otherwise.
-    const bool vec_ok = (((uintptr_t)(rowp + e0)) & 15u) == 0;
-    const int nvec = vec_ok ? n / VW : 0;
-    typename IO::vec_t regs[MAXV];
-    const typename IO::vec_t* src = (const typename IO::vec_t*)(rowp + e0);
-#pragma unroll
-    for (int j = 0; j < MAXV; ++j) {
-        int v = tid + j * NT;
-        regs[j] = typename IO::vec_t{};
-        if (v < nvec) regs[j] = src[v];
-    }
-    if (pen_on) {
-        bool bad = false;
-        for (int h = h0 + tid; h < h1; h += NT) {
-            int id = p.hids[h];
-            if (id < 0 || id >= V) { bad = true; continue; }
-            if (id >= e0 && id < e1) {
-                int o = id - e0;
-                atomicOr(&bm[o >> 5], 1u << (o & 31));
-            }
-        }
-        if (bad) atomicOr(&ctl->flags, FLAG_BAD_HISTORY);
-    }
-#pragma unroll
-    for (int j = 0; j < MAXV; ++j) {
-        int v = tid + j * NT;
-        if (v < nvec) IO::put(xs + v * VW, regs[j]);
-    }
-    for (int i = nvec * VW + tid; i < n; i += NT) xs[i] = IO::one(rowp, e0 + i);
-    __syncthreads();
-    if (pen_on) {   // sampling.py:38-45, each id once
-        for (int w = tid; w < (n + 31) / 32; w += NT) {
-            uint32_t bits = bm[w];
-            while (bits) {
-                int b = __builtin_ctz(bits);
-                bits &= bits - 1u;
-                int o = w * 32 + b;
-                xs[o] = penalize(xs[o], pen);
-            }
-        }
-        __syncthreads();
-    }
-
-    // ---- 2. per-mode chunk work
-    if (mode == MODE_GREEDY) {   // sampling.py:47-48
-        u64 best = 0;
-        for (int i = tid; i < n; i += NT) {
-            float x = xs[i];
-            uint32_t g = (x != x) ? 0xFFFFFFFFu : vkey(x);
-            u64 v = ((u64)g << 32) | (u64)(0xFFFFFFFFu - (uint32_t)(e0 + i));
-            best = v > best ? v : best;
-        }
-        best = wave_max_u64(best);
-        if (lane_id() == 0) atomicMax(&ctl->best, best);
-    } else if (mode == MODE_TOPK || mode == MODE_LARGE) {
-        uint32_t mx = 0;
-        for (int i = tid; i < n; i += NT) {
-            uint32_t s = selkey(xs[i], neg);
-            mx = s > mx ? s : mx;
-        }
-        mx = wave_max_u32(mx);
-        if (lane_id() == 0) atomicMax(&ctl->best, (u64)mx << 32);
-
-        if (mode == MODE_TOPK) {   // sampling.py:52-54, chunk-local superset
-            uint32_t theta = 0;
-            if (n > k) {
-                auto key = [&](int i) -> uint32_t { return selkey(xs[i], neg); };
-                uint32_t th = block_select_desc(n, (uint32_t)k, key, hist, 32u);
-                if (th < SK_MIN) th = SK_MIN;
-                theta = widen_threshold(th, T, neg);
-            }
-            uint32_t mine = 0;
-            for (int i = tid; i < n; i += NT) mine += selkey(xs[i], neg) >= theta ? 1u : 0u;
-            const uint32_t total = block_sum<uint32_t>(mine);
-            if (tid == 0) {
-                uint32_t base = 0xFFFFFFFFu;
-                if (total > (uint32_t)CHUNK_CAP) {
-                    atomicOr(&ctl->flags, FLAG_OVERFLOW);
-                } else {
-                    base = atomicAdd(&ctl->ncand, total);
-                    if (base + total > (uint32_t)p.capr) {
-                        atomicOr(&ctl->flags, FLAG_OVERFLOW);
-                        base = 0xFFFFFFFFu;
-                    }
-                }
-                s_base = base;
-                s_wcnt = 0;
-            }
-            __syncthreads();
-            const uint32_t base = s_base;
-            if (base != 0xFFFFFFFFu) {
-                u64* dst = p.cand + (size_t)r * (size_t)p.capr + base;
-                for (int i0 = 0; i0 < n; i0 += NT) {
-                    int i = i0 + tid;
-                    float x = 0.0f;
-                    bool keep = false;
-                    if (i < n) {
-                        x = xs[i];
-                        keep = selkey(x, neg) >= theta;
-                    }
-                    u64 mask = __ballot(keep);
-                    if (mask) {
-                        int first = __builtin_ctzll(mask);
-                        uint32_t wb = 0;
-                        if (lane_id() == first) wb = atomicAdd(&s_wcnt, (uint32_t)__builtin_popcountll(mask));
-                        wb = __shfl(wb, first, 64);
-                        if (keep) dst[wb + lanes_below(mask)] = ((u64)f2u(x) << 32) | (u64)(uint32_t)(e0 + i);
-                    }
-                }
-            }
-        }
-    }
-
-    // ---- 3. arrive; the last chunk of the row finishes it
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) s_last = (atomicAdd(&ctl->arrive, 1u) == (uint32_t)(p.NC - 1)) ? 1u : 0u;
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-
-    const uint32_t flags = __hip_atomic_load(&ctl->flags, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const u64 best = __hip_atomic_load(&ctl->best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint32_t ncand = __hip_atomic_load(&ctl->ncand, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int N = (int)off[NC];
     const float top_p = p.P[r];
     const float u = p.U ? p.U[r] : 0.0f;
     int64_t tok = -1;
     int32_t st = MXS_ROW_OK;
-    __syncthreads();
 
     if (flags & FLAG_BAD_HISTORY) {
         st = MXS_ROW_BAD_HISTORY;
@@ -709,45 +744,64 @@ __global__ __launch_bounds__(NT, 2) void k_sample(Params p)
     } else {
         bool done = false;
         if (mode == MODE_TOPK && !(flags & FLAG_OVERFLOW))
-            done = finish_topk(p, r, T, k, top_p, u, ncand, tok, st);
+            done = finish_topk(p, r, T, k, top_p, u, s_counts, off, N, tok, st);
         if (!done) {
             __syncthreads();
             finish_large<TIn>(p, r, T, k, top_p, pen, pen_on, best, u, tok, st);
         }
     }
-
     if (tid == 0) {
         p.out_tok[r] = st == MXS_ROW_OK ? tok : -1;
         if (p.out_status) p.out_status[r] = st;
-        ctl->best = 0;
-        ctl->arrive = 0;
-        ctl->ncand = 0;
-        ctl->flags = 0;
     }
-}
-
-__global__ void k_zero(uint32_t* p, size_t n)
-{
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
-        p[i] = 0u;
 }
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-int hip_status(hipError_t e) { return e == hipSuccess ? MXS_OK : MXS_ERR_HIP; }
+struct Layout {
+    size_t parts, cand_sk, cand_idx, total;
+};
+
+Layout layout(int B, int V)
+{
+    Geometry g = geometry(B, V);
+    const size_t slots = (size_t)B * (size_t)g.NC;
+    Layout L;
+    L.parts = 0;
+    L.cand_sk = align256(slots * sizeof(ChunkOut));
+    L.cand_idx = L.cand_sk + align256(slots * CHUNK_CAP * sizeof(uint32_t));
+    L.total = L.cand_idx + align256(slots * CHUNK_CAP * sizeof(uint32_t));
+    return L;
+}
+
+template <typename TIn>
+hipError_t launch(const Params& p, hipStream_t s)
+{
+    static const hipError_t a1 = hipFuncSetAttribute((const void*)k_chunks<TIn>,
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, K1_LDS_BYTES);
+    static const hipError_t a2 = hipFuncSetAttribute((const void*)k_rows<TIn>,
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, K2_LDS_BYTES);
+    (void)a1;
+    (void)a2;
+    hipLaunchKernelGGL(k_chunks<TIn>, dim3((unsigned)((long long)p.B * p.NC)), dim3(NT), K1_LDS_BYTES, s, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_rows<TIn>, dim3((unsigned)p.B), dim3(NT), K2_LDS_BYTES, s, p);
+    return hipGetLastError();
+}
 
 }  // namespace
 
 extern "C" {
 
-const char* mxs_version(void) { return "mxs-sampler 0.1.0 gfx950"; }
+const char* mxs_version(void) { return "mxs-sampler 0.2.0 gfx950"; }
 
 const char* mxs_status_string(int status)
 {
     switch (status) {
     case MXS_OK: return "ok";
     case MXS_ERR_INVALID_ARGUMENT: return "invalid argument";
-    case MXS_ERR_ALIGNMENT: return "misaligned logits, leading dimension or workspace";
+    case MXS_ERR_ALIGNMENT: return "logits not element-aligned or workspace not 256-byte aligned";
     case MXS_ERR_WORKSPACE_TOO_SMALL: return "workspace too small";
     case MXS_ERR_VOCAB_TOO_LARGE: return "vocabulary larger than MXS_MAX_VOCAB";
     case MXS_ERR_HIP: return "HIP runtime error";
@@ -755,28 +809,10 @@ const char* mxs_status_string(int status)
     }
 }
 
-size_t mxs_control_bytes(int B)
-{
-    if (B <= 0) return 0;
-    return align256((size_t)B * sizeof(RowCtl));
-}
-
 size_t mxs_workspace_bytes(int B, int V)
 {
     if (B <= 0 || V <= 0 || V > MXS_MAX_VOCAB) return 0;
-    Geometry g = geometry(B, V);
-    return mxs_control_bytes(B) + (size_t)B * (size_t)g.capr * sizeof(u64);
-}
-
-int mxs_workspace_init(void* workspace, size_t bytes, mxs_stream_t stream)
-{
-    if (!workspace || (bytes & 3)) return MXS_ERR_INVALID_ARGUMENT;
-    size_t n = bytes / 4;
-    int blocks = (int)((n + 255) / 256);
-    if (blocks > 4096) blocks = 4096;
-    if (blocks < 1) blocks = 1;
-    hipLaunchKernelGGL(k_zero, dim3(blocks), dim3(256), 0, (hipStream_t)stream, (uint32_t*)workspace, n);
-    return hip_status(hipGetLastError());
+    return layout(B, V).total;
 }
 
 int mxs_sample(const void* logits, int dtype, int B, int V, int64_t ld,
@@ -797,9 +833,10 @@ int mxs_sample(const void* logits, int dtype, int B, int V, int64_t ld,
     if (ld < V) return MXS_ERR_INVALID_ARGUMENT;
     const uintptr_t esize = dtype == MXS_DTYPE_F32 ? 4u : 2u;
     if (((uintptr_t)logits & (esize - 1u)) || ((uintptr_t)workspace & 255u)) return MXS_ERR_ALIGNMENT;
-    if (workspace_bytes < mxs_workspace_bytes(B, V)) return MXS_ERR_WORKSPACE_TOO_SMALL;
+    const Layout L = layout(B, V);
+    if (workspace_bytes < L.total) return MXS_ERR_WORKSPACE_TOO_SMALL;
 
-    Geometry g = geometry(B, V);
+    const Geometry g = geometry(B, V);
     Params p;
     p.logits = logits;
     p.B = B;
@@ -807,7 +844,6 @@ int mxs_sample(const void* logits, int dtype, int B, int V, int64_t ld,
     p.ld = ld;
     p.CS = g.CS;
     p.NC = g.NC;
-    p.capr = g.capr;
     p.T = temperature;
     p.K = top_k;
     p.P = top_p;
@@ -818,23 +854,14 @@ int mxs_sample(const void* logits, int dtype, int B, int V, int64_t ld,
     p.out_tok = out_tokens;
     p.out_status = out_status;
     p.out_probs = out_probs;
-    p.ctl = (RowCtl*)workspace;
-    p.cand = (u64*)((char*)workspace + mxs_control_bytes(B));
+    char* ws = (char*)workspace;
+    p.parts = (ChunkOut*)(ws + L.parts);
+    p.cand_sk = (uint32_t*)(ws + L.cand_sk);
+    p.cand_idx = (uint32_t*)(ws + L.cand_idx);
 
-    const dim3 grid((unsigned)((long long)B * g.NC));
     hipStream_t s = (hipStream_t)stream;
-    if (dtype == MXS_DTYPE_F32) {
-        static const hipError_t attr = hipFuncSetAttribute(
-            (const void*)k_sample<float>, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
-        (void)attr;
-        hipLaunchKernelGGL(k_sample<float>, grid, dim3(NT), LDS_BYTES, s, p);
-    } else {
-        static const hipError_t attr = hipFuncSetAttribute(
-            (const void*)k_sample<__half>, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
-        (void)attr;
-        hipLaunchKernelGGL(k_sample<__half>, grid, dim3(NT), LDS_BYTES, s, p);
-    }
-    return hip_status(hipGetLastError());
+    hipError_t e = dtype == MXS_DTYPE_F32 ? launch<float>(p, s) : launch<__half>(p, s);
+    return e == hipSuccess ? MXS_OK : MXS_ERR_HIP;
 }
 
 }  // extern "C"

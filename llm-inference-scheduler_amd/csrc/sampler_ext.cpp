@@ -44,18 +44,6 @@ int64_t workspace_bytes(int64_t B, int64_t V)
     return (int64_t)mxs_workspace_bytes((int)B, (int)V);
 }
 
-int64_t control_bytes(int64_t B) { return (int64_t)mxs_control_bytes((int)B); }
-
-void workspace_init(torch::Tensor ws)
-{
-    TORCH_CHECK(ws.is_cuda() && ws.is_contiguous() && ws.scalar_type() == torch::kUInt8,
-                "workspace must be a contiguous uint8 device tensor");
-    const c10::DeviceGuard guard(ws.device());
-    auto stream = c10::hip::getCurrentHIPStream();
-    raise_status(mxs_workspace_init(ws.data_ptr(), (size_t)ws.numel(), (mxs_stream_t)stream.stream()),
-                 "mxs_workspace_init");
-}
-
 void sample(torch::Tensor logits, torch::Tensor temperature, torch::Tensor top_k,
             torch::Tensor top_p, torch::Tensor penalty,
             std::optional<torch::Tensor> hist_offsets, std::optional<torch::Tensor> hist_ids,
@@ -114,8 +102,6 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m)
     m.doc() = "MI355X sampler chain: torch front end of the mxs_sampler C ABI";
     m.def("version", &version);
     m.def("workspace_bytes", &workspace_bytes, "workspace size for a [B, V] batch");
-    m.def("control_bytes", &control_bytes, "size of the workspace control area for B rows");
-    m.def("workspace_init", &workspace_init, "zero a workspace (or its control area) on the current stream");
     m.def("sample", &sample, "sample one token per row (see mxs_sampler.h)",
           py::arg("logits"), py::arg("temperature"), py::arg("top_k"), py::arg("top_p"),
           py::arg("penalty"), py::arg("hist_offsets"), py::arg("hist_ids"), py::arg("uniforms"),

@@ -8,11 +8,12 @@ mini_engine/sampling.py, on hand-written gfx950 HIP kernels.
 """
 
 from .batch import (MAX_VOCAB, ROW_BAD_HISTORY, ROW_BAD_PARAM, ROW_EMPTY_NUCLEUS,
-                    ROW_NONFINITE, ROW_OK, pack_requests, sample_batch, sample_requests)
+                    ROW_NONFINITE, ROW_OK, Sampler, pack_requests, sample_batch,
+                    sample_requests)
 from .sampling import SamplingParams, sample
 
 __all__ = [
-    "SamplingParams", "sample", "sample_batch", "sample_requests", "pack_requests",
+    "SamplingParams", "sample", "sample_batch", "Sampler", "sample_requests", "pack_requests",
     "MAX_VOCAB", "ROW_OK", "ROW_BAD_HISTORY", "ROW_BAD_PARAM", "ROW_NONFINITE",
     "ROW_EMPTY_NUCLEUS",
 ]

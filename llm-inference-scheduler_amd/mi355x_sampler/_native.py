@@ -47,30 +47,14 @@ _workspaces: dict = {}
 
 
 def workspace(device: torch.device, B: int, V: int) -> torch.Tensor:
-    """A ready workspace for a [B, V] call on `device` and its current stream.
-
-    Kernels leave the control area (per-row counters at the front) zeroed after
-    each call, so consecutive calls with the same B reuse the workspace as is.
-    A call with another B stores candidate lists where this B's counters lie,
-    so the control area is zeroed again whenever B changes.  One workspace per
-    (device, stream) keeps calls on different streams apart.
-    """
-    ext = extension()
-    need = int(ext.workspace_bytes(B, V))
+    """A workspace of at least mxs_workspace_bytes(B, V) bytes for `device`
+    and its current stream (one per (device, stream), grown on demand).  The
+    kernels need it neither zeroed nor preserved between calls."""
+    need = int(extension().workspace_bytes(B, V))
     stream = torch.cuda.current_stream(device)
     key = (device.index, stream.cuda_stream)
-    ent = _workspaces.get(key)
-    if ent is None or ent[0].numel() < need:
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < need:
         ws = torch.empty(max(need, 256), dtype=torch.uint8, device=device)
-        ext.workspace_init(ws)
-        ent = [ws, B]
-        _workspaces[key] = ent
-    elif ent[1] != B:
-        ext.workspace_init(ent[0][: int(ext.control_bytes(B))])
-        ent[1] = B
-    return ent[0]
-
-
-def reset_workspaces() -> None:
-    """Forget cached workspaces (e.g. after a failed launch left one dirty)."""
-    _workspaces.clear()
+        _workspaces[key] = ws
+    return ws

@@ -51,6 +51,32 @@ def sample_batch(logits: torch.Tensor, temperature: torch.Tensor, top_k: torch.T
     return (tokens, status) if return_status else tokens
 
 
+class Sampler:
+    """Preallocated outputs and workspace for repeated [B, V] launches.
+
+    For serving loops: `run()` is one asynchronous launch on the current
+    stream with no allocation, so back-to-back steps keep the GPU busy.
+    """
+
+    def __init__(self, B: int, V: int, device, with_probs: bool = False):
+        self.device = torch.device(device)
+        _native.require_gpu(self.device)
+        self.ext = _native.extension()
+        self.B, self.V = B, V
+        self.tokens = torch.empty(B, dtype=torch.int64, device=self.device)
+        self.status = torch.empty(B, dtype=torch.int32, device=self.device)
+        self.probs = (torch.zeros((B, V), dtype=torch.float32, device=self.device)
+                      if with_probs else None)
+        self.workspace = torch.empty(max(int(self.ext.workspace_bytes(B, V)), 256),
+                                     dtype=torch.uint8, device=self.device)
+
+    def run(self, logits, temperature, top_k, top_p, penalty, hist_offsets=None,
+            hist_ids=None, uniforms=None):
+        self.ext.sample(logits, temperature, top_k, top_p, penalty, hist_offsets, hist_ids,
+                        uniforms, self.tokens, self.status, self.probs, self.workspace)
+        return self.tokens
+
+
 def _normalize_history(ids: Sequence[int], V: int) -> list:
     """torch indexing rules of sampling.py:39-40: negative ids wrap once,
     anything else out of range raises IndexError."""
