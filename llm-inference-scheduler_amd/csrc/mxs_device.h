@@ -21,7 +21,7 @@ constexpr int CS_MAX = 16384;           // logits staged in LDS per chunk
 constexpr int CS_MIN = 2048;
 constexpr int NC_MAX = 255;             // chunks per row
 constexpr int KMAX = 1024;              // largest top_k served by the candidate path
-constexpr int CHUNK_CAP = 2048;         // candidates one chunk may emit
+constexpr int CHUNK_CAP = 4096;         // candidates one chunk may emit
 constexpr int CAND_LDS = 16384;         // candidate keys the finisher keeps in LDS
 constexpr int SORT_CAP = 4096;          // top-k survivors sorted in LDS (= 8 per thread)
 constexpr int LCAP = 4096;              // elements collected per refinement step (= 8 per thread)
@@ -29,9 +29,9 @@ constexpr int MASS_SHIFT = 20;          // masses carry 44 fractional bits: 24-b
 constexpr uint32_t SK_MIN = 0x007FFFFFu;  // selection key of -inf (T > 0) or +inf (T < 0)
 
 // LDS map of the chunk kernel (dynamic shared memory).
-constexpr int K1_XS = 0;                        // CS_MAX fp32 logits
-constexpr int K1_HIST = K1_XS + 4 * CS_MAX;     // 2048 x u32 radix histogram
-constexpr int K1_BM = K1_HIST + 8192;           // CS_MAX bits of penalty bitmap
+constexpr int K1_KS = 0;                        // 4 * NT group-extreme keys
+constexpr int K1_HIST = K1_KS + 16 * NT;        // 2048 x u32 histogram
+constexpr int K1_BM = K1_HIST + 8192;           // CS_MAX bits of history bitmap
 constexpr int K1_LDS_BYTES = K1_BM + CS_MAX / 8;
 
 // LDS map of the row kernel.
@@ -223,11 +223,11 @@ __device__ BinHit find_desc(const T* h, int nb, u64 t)
     const int per = nb / NT;
     const int b0 = threadIdx.x * per;
     if (threadIdx.x == 0) s_hit = BinHit{0, 0};   // ordered before the search by the scan's barriers
-    u64 mine = 0;
-    for (int i = 0; i < per; ++i) mine += (u64)h[b0 + i];
-    u64 total;
-    u64 incl = block_incl_scan<u64>(mine, &total);
-    u64 a = total - incl;   // mass of bins above this thread's range
+    T mine = 0;
+    for (int i = 0; i < per; ++i) mine += h[b0 + i];
+    T total;
+    T incl = block_incl_scan<T>(mine, &total);
+    u64 a = (u64)(total - incl);   // sum of the bins above this thread's range
     for (int b = b0 + per - 1; b >= b0; --b) {
         u64 hb = (u64)h[b];
         if (a <= t && t < a + hb) s_hit = BinHit{b, a};

@@ -4,14 +4,16 @@
 // Here one call samples a whole [B, V] batch with two launches:
 //
 // k_chunks  grid B x NC, workgroup (r, c) owns chunk c of row r (<= 16384
-//           logits).  It streams the chunk from HBM once in 128-bit loads into
-//           LDS (fp16 upcast to fp32 there), applies the repetition penalty in
-//           place for the history ids inside the chunk (an LDS bitmap marks
-//           each id once), then per row mode:
-//             greedy  chunk argmax as a packed (key, ~index)
-//             top-k   MSD radix select on order-preserving keys for the
-//                     chunk's k-th largest, widened over the rounding of x / T,
-//                     and the survivors written to the chunk's candidate slot
+//           logits, 32 per thread).  It streams the chunk from HBM once in
+//           128-bit loads into registers (fp16 upcast to fp32 there) and marks
+//           the history ids inside the chunk in an LDS bitmap (each id once).
+//           Then per row mode:
+//             greedy  argmax of the penalized chunk as a packed (key, ~index)
+//             top-k   a lower bound on the chunk's k'-th largest raw value from
+//                     the extremes of groups of 8 (k' = k + history ids in the chunk),
+//                     widened over the rounding of x / T; the elements above it
+//                     and every history id are written, with penalized values,
+//                     to the chunk's candidate slot
 //             other   chunk maximum only
 //           Results go to fixed per-(row, chunk) slots: no atomics, no
 //           cross-workgroup waits, nothing to clear between calls.
@@ -40,7 +42,7 @@ struct ChunkOut {          // one slot per (row, chunk), 16 bytes
 };
 static_assert(sizeof(ChunkOut) == 16, "ChunkOut layout");
 
-enum : uint32_t { FLAG_BAD_HISTORY = 1u, FLAG_OVERFLOW = 2u };
+enum : uint32_t { FLAG_BAD_HISTORY = 1u, FLAG_OVERFLOW = 2u, FLAG_NAN = 4u };
 enum RowMode { MODE_GREEDY = 0, MODE_TOPK = 1, MODE_LARGE = 2, MODE_INVALID = 3 };
 
 struct Params {
@@ -96,6 +98,7 @@ template <> struct VecIO<float> {
     static constexpr int W = 4;
     typedef float4 vec_t;
     __device__ static void put(float* dst, const vec_t& v) { *(float4*)dst = v; }
+    __device__ static void unpack(const vec_t& v, float* d) { d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w; }
     __device__ static float one(const float* p, int i) { return p[i]; }
 };
 template <> struct VecIO<__half> {
@@ -114,6 +117,13 @@ template <> struct VecIO<__half> {
         b.z = h2f(v.w & 0xFFFFu); b.w = h2f(v.w >> 16);
         *(float4*)dst = a;
         *(float4*)(dst + 4) = b;
+    }
+    __device__ static void unpack(const vec_t& v, float* d)
+    {
+        d[0] = h2f(v.x & 0xFFFFu); d[1] = h2f(v.x >> 16);
+        d[2] = h2f(v.y & 0xFFFFu); d[3] = h2f(v.y >> 16);
+        d[4] = h2f(v.z & 0xFFFFu); d[5] = h2f(v.z >> 16);
+        d[6] = h2f(v.w & 0xFFFFu); d[7] = h2f(v.w >> 16);
     }
     __device__ static float one(const __half* p, int i)
     {
@@ -162,15 +172,119 @@ __device__ uint32_t widen_threshold(uint32_t th, float T, bool neg)
 
 // ================================================================ k_chunks
 
+struct Reduced {
+    uint32_t max, min, any;
+};
+
+// One barrier round: max of a, min of b, OR of c over the workgroup.
+__device__ Reduced block_reduce(uint32_t a, uint32_t b, uint32_t c)
+{
+    __shared__ uint32_t s[3][NWAVES];
+    for (int o = 32; o > 0; o >>= 1) {
+        const uint32_t a2 = __shfl_xor(a, o, 64), b2 = __shfl_xor(b, o, 64), c2 = __shfl_xor(c, o, 64);
+        a = a2 > a ? a2 : a;
+        b = b2 < b ? b2 : b;
+        c |= c2;
+    }
+    __syncthreads();
+    if (lane_id() == 0) { s[0][wave_id()] = a; s[1][wave_id()] = b; s[2][wave_id()] = c; }
+    __syncthreads();
+    Reduced r{s[0][0], s[1][0], s[2][0]};
+#pragma unroll
+    for (int i = 1; i < NWAVES; ++i) {
+        r.max = s[0][i] > r.max ? s[0][i] : r.max;
+        r.min = s[1][i] < r.min ? s[1][i] : r.min;
+        r.any |= s[2][i];
+    }
+    return r;
+}
+
+// The r-th largest (0-based) of the cb <= 64 keys of ks[0 .. 4*NT) that fall
+// in histogram bin `bin` ((key - lo) >> sh == bin): gathered into one wave and
+// ranked by shuffles.  `fallback` is returned if the gather disagrees.
+__device__ uint32_t exact_in_bin(const uint32_t* ks, uint32_t lo, int sh, uint32_t bin, uint32_t cb,
+                                 uint32_t r, uint32_t fallback)
+{
+    __shared__ uint32_t s_keys[64];
+    __shared__ uint32_t s_n, s_res;
+    if (threadIdx.x == 0) { s_n = 0; s_res = fallback; }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t key = ks[4 * threadIdx.x + i];
+        if (((key - lo) >> sh) == bin) {
+            const uint32_t o = atomicAdd(&s_n, 1u);
+            if (o < 64u) s_keys[o] = key;
+        }
+    }
+    __syncthreads();
+    if (wave_id() == 0 && s_n == cb) {
+        const uint32_t lane = (uint32_t)lane_id();
+        const uint32_t mine = lane < cb ? s_keys[lane] : 0u;
+        uint32_t gt = 0, ge = 0;
+        for (uint32_t t = 0; t < cb; ++t) {
+            const uint32_t o = __shfl(mine, (int)t, 64);
+            gt += o > mine ? 1u : 0u;
+            ge += o >= mine ? 1u : 0u;
+        }
+        const bool hit = lane < cb && gt <= r && r < ge;
+        const u64 mask = __ballot(hit);
+        if (mask && lane == (uint32_t)__builtin_ctzll(mask)) s_res = mine;
+    }
+    __syncthreads();
+    const uint32_t res = s_res;
+    __syncthreads();
+    return res;
+}
+
+constexpr int EPT = CS_MAX / NT;   // logits per thread per chunk (32)
+
+// Chunk element (j, q) of this thread: local index (tid + j*NT) * VW + q.
+template <typename TIn>
+__device__ __forceinline__ void load_chunk(const TIn* rowp, int e0, int n, float pad, float (&x)[EPT])
+{
+    typedef VecIO<TIn> IO;
+    constexpr int VW = IO::W;
+    constexpr int MAXV = EPT / VW;
+    const int tid = threadIdx.x;
+    // 128-bit loads when the chunk start is 16-byte aligned (every chunk of a
+    // row whose start is: CS is a multiple of 8 elements), scalar otherwise.
+    const bool vec_ok = (((uintptr_t)(rowp + e0)) & 15u) == 0;
+    const int nvec = vec_ok ? n / VW : 0;
+    const typename IO::vec_t* src = (const typename IO::vec_t*)(rowp + e0);
+    typename IO::vec_t regs[MAXV];
+#pragma unroll
+    for (int j = 0; j < MAXV; ++j) {
+        const int v = tid + j * NT;
+        regs[j] = typename IO::vec_t{};
+        if (v < nvec) regs[j] = src[v];
+    }
+#pragma unroll
+    for (int j = 0; j < MAXV; ++j) {
+        const int v = tid + j * NT;
+        if (v < nvec) {
+            IO::unpack(regs[j], &x[j * VW]);
+        } else {
+#pragma unroll
+            for (int q = 0; q < VW; ++q) {
+                const int e = v * VW + q;
+                x[j * VW + q] = e < n ? IO::one(rowp, e0 + e) : pad;
+            }
+        }
+    }
+}
+
 template <typename TIn>
 __global__ __launch_bounds__(NT, 2) void k_chunks(Params p)
 {
     extern __shared__ __align__(16) unsigned char smem[];
-    float* xs = (float*)(smem + K1_XS);
-    uint32_t* hist = (uint32_t*)(smem + K1_HIST);
-    uint32_t* bm = (uint32_t*)(smem + K1_BM);
-    __shared__ uint32_t s_wcnt;
+    uint32_t* ks = (uint32_t*)(smem + K1_KS);      // 4 * NT per-thread group keys
+    uint32_t* hist = (uint32_t*)(smem + K1_HIST);  // 2048 bins
+    uint32_t* bm = (uint32_t*)(smem + K1_BM);      // CS_MAX bits
 
+    typedef VecIO<TIn> IO;
+    constexpr int VW = IO::W;
+    constexpr int MAXV = EPT / VW;
     const int tid = threadIdx.x;
     const int r = blockIdx.x / p.NC;
     const int c = blockIdx.x - r * p.NC;
@@ -188,33 +302,22 @@ __global__ __launch_bounds__(NT, 2) void k_chunks(Params p)
     const int h1 = p.hoff ? p.hoff[r + 1] : 0;
     const bool pen_on = (pen != 1.0f) && (h1 > h0);
     const size_t slot = (size_t)blockIdx.x;
+    auto local = [&](int j, int q) { return (tid + j * NT) * VW + q; };
 
     if (p.out_probs) {
         float* o = p.out_probs + (size_t)r * (size_t)V;
         for (int i = e0 + tid; i < e1; i += NT) o[i] = 0.0f;
     }
 
-    // ---- stream the chunk into LDS; penalty bitmap from the history
-    typedef VecIO<TIn> IO;
-    constexpr int VW = IO::W;
-    constexpr int MAXV = CS_MAX / (NT * VW);
-    if (pen_on)
-        for (int w = tid; w < CS_MAX / 32; w += NT) bm[w] = 0;
-    __syncthreads();
-    // 128-bit loads when the chunk start is 16-byte aligned (every chunk of a
-    // row whose start is: CS is a multiple of 8 elements), scalar otherwise.
-    const bool vec_ok = (((uintptr_t)(rowp + e0)) & 15u) == 0;
-    const int nvec = vec_ok ? n / VW : 0;
-    typename IO::vec_t regs[MAXV];
-    const typename IO::vec_t* src = (const typename IO::vec_t*)(rowp + e0);
-#pragma unroll
-    for (int j = 0; j < MAXV; ++j) {
-        int v = tid + j * NT;
-        regs[j] = typename IO::vec_t{};
-        if (v < nvec) regs[j] = src[v];
-    }
+    float x[EPT];
+    load_chunk<TIn>(rowp, e0, n, neg ? INFINITY : -INFINITY, x);   // padding is never selected
+
+    // ---- history ids inside the chunk, once each (sampling.py:39 sorted(set()))
     uint32_t flags = 0;
+    uint32_t hc = 0;   // distinct history ids in this chunk
     if (pen_on) {
+        bm[tid] = 0;   // NT words = CS_MAX bits
+        __syncthreads();
         bool bad = false;
         for (int h = h0 + tid; h < h1; h += NT) {
             int id = p.hids[h];
@@ -224,88 +327,146 @@ __global__ __launch_bounds__(NT, 2) void k_chunks(Params p)
                 atomicOr(&bm[o >> 5], 1u << (o & 31));
             }
         }
-        if (block_sum<uint32_t>(bad ? 1u : 0u)) flags |= FLAG_BAD_HISTORY;
-    }
-#pragma unroll
-    for (int j = 0; j < MAXV; ++j) {
-        int v = tid + j * NT;
-        if (v < nvec) IO::put(xs + v * VW, regs[j]);
-    }
-    for (int i = nvec * VW + tid; i < n; i += NT) xs[i] = IO::one(rowp, e0 + i);
-    __syncthreads();
-    if (pen_on) {   // sampling.py:38-45, each id once
-        for (int w = tid; w < (n + 31) / 32; w += NT) {
-            uint32_t bits = bm[w];
-            while (bits) {
-                int b = __builtin_ctz(bits);
-                bits &= bits - 1u;
-                int o = w * 32 + b;
-                xs[o] = penalize(xs[o], pen);
-            }
-        }
         __syncthreads();
+        hc = block_sum<uint32_t>((uint32_t)__builtin_popcount(bm[tid]));
+        if (block_max<uint32_t>(bad ? 1u : 0u)) flags |= FLAG_BAD_HISTORY;
     }
 
-    // ---- per-mode chunk work
+    // bit i of hm: element x[i] of this thread is a history id
+    uint32_t hm = 0;
+    if (pen_on) {
+#pragma unroll
+        for (int j = 0; j < MAXV; ++j) {
+            const int eb = local(j, 0);
+            hm |= ((bm[eb >> 5] >> (eb & 31)) & ((1u << VW) - 1u)) << (j * VW);
+        }
+    }
+
     u64 best = 0;
     uint32_t count = 0;
-    if (mode == MODE_GREEDY) {   // sampling.py:47-48
-        u64 b = 0;
-        for (int i = tid; i < n; i += NT) {
-            float x = xs[i];
-            uint32_t g = (x != x) ? 0xFFFFFFFFu : vkey(x);
-            u64 v = ((u64)g << 32) | (u64)(0xFFFFFFFFu - (uint32_t)(e0 + i));
-            b = v > b ? v : b;
+    if (mode == MODE_GREEDY) {   // sampling.py:45-48: argmax of the penalized row
+        if (hm) {
+#pragma unroll
+            for (int i = 0; i < EPT; ++i)
+                if ((hm >> i) & 1u) x[i] = penalize(x[i], pen);
         }
-        best = block_max<u64>(b);
+        uint32_t bk = 0, bi = 0;
+#pragma unroll
+        for (int j = 0; j < MAXV; ++j)
+#pragma unroll
+            for (int q = 0; q < VW; ++q) {
+                const int e = local(j, q);
+                const float v = x[j * VW + q];
+                const uint32_t g = (v != v) ? 0xFFFFFFFFu : vkey(v);
+                if (e < n && g > bk) { bk = g; bi = (uint32_t)e; }   // ascending e: first max wins
+            }
+        const u64 mine = bk ? (((u64)bk << 32) | (u64)(0xFFFFFFFFu - (uint32_t)e0 - bi)) : 0ull;
+        best = block_max<u64>(mine);
     } else if (mode == MODE_TOPK || mode == MODE_LARGE) {
-        uint32_t mx = 0;
-        for (int i = tid; i < n; i += NT) {
-            uint32_t s = selkey(xs[i], neg);
-            mx = s > mx ? s : mx;
+        // NaN check: a sum of the chunk is finite unless it holds a NaN or an
+        // infinity (padding included); only then look element by element.
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) acc += x[i];
+        uint32_t nan_any = 0;
+        if (!isfinite(acc)) {
+#pragma unroll
+            for (int i = 0; i < EPT; ++i) nan_any |= (x[i] != x[i]) ? 1u : 0u;
         }
-        best = (u64)block_max<uint32_t>(mx) << 32;
 
-        if (mode == MODE_TOPK) {   // sampling.py:52-54, a superset of the chunk's share
+        // The extreme of each group of 8 logits in the order of x / T
+        // (max for T > 0, min for T < 0); NaNs never win.
+        constexpr int G = EPT / 8;
+        uint32_t gk[G];
+        uint32_t gmax = 0, gmin = 0xFFFFFFFFu;
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+            float a = x[8 * i];
+            if (!neg) {
+#pragma unroll
+                for (int q = 1; q < 8; ++q) a = fmaxf(a, x[8 * i + q]);
+            } else {
+#pragma unroll
+                for (int q = 1; q < 8; ++q) a = fminf(a, x[8 * i + q]);
+            }
+            gk[i] = (a != a) ? SK_MIN : selkey(a, neg);
+            gmax = gk[i] > gmax ? gk[i] : gmax;
+            gmin = gk[i] < gmin ? gk[i] : gmin;
+        }
+        const Reduced rd = block_reduce(gmax, gmin, nan_any);
+        if (rd.any) flags |= FLAG_NAN;
+        best = (u64)rd.max << 32;
+
+        if (mode == MODE_TOPK) {
+            // sampling.py:52-54.  The group extremes are values of distinct
+            // elements, so with k' = k + (history ids in the chunk) the k'-th
+            // largest of these 4*NT keys bounds the chunk's k'-th largest raw
+            // key from below, and every element of the penalized top-k is a
+            // history id or at least that large.  Candidates: raw keys at or
+            // above the bound (widened over the rounding of x / T); then every
+            // history id with its raw key, in a second segment whose keys the
+            // row kernel penalizes.
+            const uint32_t kp = (uint32_t)k + hc;
             uint32_t theta = 0;
-            if (n > k) {
-                auto key = [&](int i) -> uint32_t { return selkey(xs[i], neg); };
-                uint32_t th = block_select_desc(n, (uint32_t)k, key, hist, 32u);
+            if ((uint32_t)n > kp && kp <= (uint32_t)(G * NT)) {
+#pragma unroll
+                for (int i = 0; i < G; ++i) ks[G * tid + i] = gk[i];
+                const uint32_t lo = rd.min;
+                const uint32_t span = rd.max - lo;
+                const int sh = span >= 2048u ? (32 - __builtin_clz(span)) - 11 : 0;
+                for (int b = tid; b < 2048; b += NT) hist[b] = 0;
+                __syncthreads();
+#pragma unroll
+                for (int i = 0; i < G; ++i) atomicAdd(&hist[(gk[i] - lo) >> sh], 1u);
+                __syncthreads();
+                const BinHit hit = find_desc<uint32_t>(hist, 2048, (u64)(kp - 1u));
+                uint32_t th = lo + ((uint32_t)hit.bin << sh);   // the bin's lower edge bounds it
+                const uint32_t cb = hist[hit.bin];
+                if (sh > 0 && cb <= 64u)                           // exact: rank the bin's keys
+                    th = exact_in_bin(ks, lo, sh, (uint32_t)hit.bin, cb, kp - 1u - (uint32_t)hit.above, th);
                 if (th < SK_MIN) th = SK_MIN;
                 theta = widen_threshold(th, T, neg);
             }
-            uint32_t mine = 0;
-            for (int i = tid; i < n; i += NT) mine += selkey(xs[i], neg) >= theta ? 1u : 0u;
-            const uint32_t total = block_sum<uint32_t>(mine);
-            if (total > (uint32_t)CHUNK_CAP) {
+            uint32_t cm = 0;   // raw candidates among my elements
+            if (theta <= SK_MIN) {   // the whole chunk
+#pragma unroll
+                for (int j = 0; j < MAXV; ++j)
+#pragma unroll
+                    for (int q = 0; q < VW; ++q)
+                        cm |= (local(j, q) < n ? 1u : 0u) << (j * VW + q);
+            } else if (!neg) {
+                const float xth = sel_inv(theta, false);
+#pragma unroll
+                for (int i = 0; i < EPT; ++i) cm |= (x[i] >= xth ? 1u : 0u) << i;
+            } else {
+                const float xth = sel_inv(theta, true);
+#pragma unroll
+                for (int i = 0; i < EPT; ++i) cm |= (x[i] <= xth ? 1u : 0u) << i;
+            }
+            const uint32_t emit = cm | hm;
+            const uint32_t c1 = (uint32_t)__builtin_popcount(cm & ~hm);
+            const uint32_t c2 = (uint32_t)__builtin_popcount(hm);
+            uint32_t tot;
+            const uint32_t pre = block_incl_scan<uint32_t>(c1 | (c2 << 16), &tot) - (c1 | (c2 << 16));
+            const uint32_t C1 = tot & 0xFFFFu, C2 = tot >> 16;
+            if (C1 + C2 > (uint32_t)CHUNK_CAP) {
                 flags |= FLAG_OVERFLOW;
             } else {
-                count = total;
-                if (tid == 0) s_wcnt = 0;
-                __syncthreads();
+                count = C1 | (C2 << 16);
+                uint32_t o1 = pre & 0xFFFFu, o2 = C1 + (pre >> 16);
                 uint32_t* dsk = p.cand_sk + slot * CHUNK_CAP;
                 uint32_t* didx = p.cand_idx + slot * CHUNK_CAP;
-                for (int i0 = 0; i0 < n; i0 += NT) {
-                    int i = i0 + tid;
-                    uint32_t s = 0;
-                    bool keep = false;
-                    if (i < n) {
-                        s = selkey(xs[i], neg);
-                        keep = s >= theta;
-                    }
-                    u64 mask = __ballot(keep);
-                    if (mask) {
-                        int first = __builtin_ctzll(mask);
-                        uint32_t wb = 0;
-                        if (lane_id() == first) wb = atomicAdd(&s_wcnt, (uint32_t)__builtin_popcountll(mask));
-                        wb = __shfl(wb, first, 64);
-                        if (keep) {
-                            uint32_t o = wb + lanes_below(mask);
-                            dsk[o] = s;
-                            didx[o] = (uint32_t)(e0 + i);
+#pragma unroll
+                for (int j = 0; j < MAXV; ++j)
+#pragma unroll
+                    for (int q = 0; q < VW; ++q) {
+                        const int i = j * VW + q;
+                        if ((emit >> i) & 1u) {
+                            const uint32_t o = ((hm >> i) & 1u) ? o2++ : o1++;
+                            dsk[o] = selkey(x[i], neg);
+                            didx[o] = (uint32_t)(e0 + local(j, q));
                         }
                     }
-                }
             }
         }
     }
@@ -507,7 +668,17 @@ __device__ void finish_large(const Params& p, int r, float T, int k, float top_p
         __syncthreads();
     }
 
-    const float m = sel_inv((uint32_t)(best >> 32), L.neg) / T;
+    // the chunks' maximum is over raw logits; with a penalty take it again
+    uint32_t skmax = (uint32_t)(best >> 32);
+    if (pen_on) {
+        uint32_t mx = 0;
+        for (int i = threadIdx.x; i < V; i += NT) {
+            const uint32_t sk = selkey(L.x_at(i), L.neg);
+            mx = sk > mx ? sk : mx;
+        }
+        skmax = block_max<uint32_t>(mx);
+    }
+    const float m = sel_inv(skmax, L.neg) / T;
     if (!isfinite(m)) { st = MXS_ROW_NONFINITE; tok = -1; return; }
     L.m = m;
 
@@ -556,7 +727,11 @@ __device__ void finish_large(const Params& p, int r, float T, int k, float top_p
 // Top-k rows.  The chunks' candidates hold every element whose tempered
 // value reaches the row's k-th largest.  Returns false when the survivors do
 // not fit the LDS sort; the caller then takes the multi-pass path.
-__device__ bool finish_topk(const Params& p, int r, float T, int k, float top_p, float u,
+//
+// Each thread owns a slice of one chunk's candidate slot (NT / NC threads per
+// chunk) and moves it in unrolled batches, so a batch costs one memory round
+// trip rather than one per element.
+__device__ bool finish_topk(const Params& p, int r, float T, int k, float top_p, float pen, float u,
                             const uint32_t* counts, const uint32_t* off, int N,
                             int64_t& tok, int32_t& st)
 {
@@ -565,29 +740,46 @@ __device__ bool finish_topk(const Params& p, int r, float T, int k, float top_p,
     u64* keys = (u64*)(smem + K2_B);                  // SORT_CAP sort keys
     u64* cum = (u64*)(smem + K2_B + 8 * SORT_CAP);    // SORT_CAP prefix masses
     uint32_t* hist = (uint32_t*)(smem + K2_HIST);
-    __shared__ uint32_t s_n;
+    constexpr int BATCH = 16;
     const int NC = p.NC, V = p.V;
     const bool neg = T < 0.0f;
     const uint32_t kk = (uint32_t)(k < V ? k : V);
-    const size_t slot0 = (size_t)r * NC;
+    const int tpc = NT / NC;
+    const int mc = threadIdx.x / tpc;                 // my chunk (>= NC: idle)
+    const int ml = threadIdx.x - mc * tpc;            // my lane within it
+    const bool active = mc < NC;
+    // a chunk's slot holds its raw candidates, then its history ids with raw
+    // keys: those get the penalty (sampling.py:42-45) here
+    const int mc1 = active ? (int)(counts[mc] & 0xFFFFu) : 0;
+    const int mcnt = active ? mc1 + (int)(counts[mc] >> 16) : 0;
+    auto penalized = [&](uint32_t sk) -> uint32_t { return selkey(penalize(sel_inv(sk, neg), pen), neg); };
+    const size_t mslot = ((size_t)r * NC + (active ? mc : 0)) * CHUNK_CAP;
+    const uint32_t* gsk = p.cand_sk + mslot;
+    const uint32_t* gidx = p.cand_idx + mslot;
     const bool in_lds = N <= CAND_LDS;
+    uint32_t* mck = ck + (active ? off[mc] : 0);
 
     if (in_lds) {
-        for (int c = 0; c < NC; ++c) {
-            const uint32_t* src = p.cand_sk + (slot0 + c) * CHUNK_CAP;
-            for (int j = threadIdx.x; j < (int)counts[c]; j += NT) ck[off[c] + j] = src[j];
+        for (int j0 = ml; j0 < mcnt; j0 += BATCH * tpc) {
+            uint32_t v[BATCH];
+#pragma unroll
+            for (int b = 0; b < BATCH; ++b) {
+                const int j = j0 + b * tpc;
+                v[b] = j < mcnt ? gsk[j] : 0u;
+            }
+#pragma unroll
+            for (int b = 0; b < BATCH; ++b) {
+                const int j = j0 + b * tpc;
+                if (j < mcnt) mck[j] = j < mc1 ? v[b] : penalized(v[b]);
+            }
         }
         __syncthreads();
     }
+    auto key_at = [&](int j) -> uint32_t {
+        return in_lds ? mck[j] : (j < mc1 ? gsk[j] : penalized(gsk[j]));
+    };
     auto visit = [&](auto&& f) {
-        if (in_lds) {
-            for (int i = threadIdx.x; i < N; i += NT) f(ck[i]);
-        } else {
-            for (int c = 0; c < NC; ++c) {
-                const uint32_t* src = p.cand_sk + (slot0 + c) * CHUNK_CAP;
-                for (int j = threadIdx.x; j < (int)counts[c]; j += NT) f(src[j]);
-            }
-        }
+        for (int j = ml; j < mcnt; j += tpc) f(key_at(j));
     };
 
     // sampling.py:52-54: the k-th largest, then everything that rounds onto it
@@ -596,34 +788,26 @@ __device__ bool finish_topk(const Params& p, int r, float T, int k, float top_p,
     const uint32_t theta = widen_threshold(sk_k, T, neg);
     uint32_t mine = 0;
     visit([&](uint32_t s) { mine += s >= theta ? 1u : 0u; });
-    const int n1 = (int)block_sum<uint32_t>(mine);
+    uint32_t n1u;
+    uint32_t o = block_incl_scan<uint32_t>(mine, &n1u) - mine;
+    const int n1 = (int)n1u;
     if (n1 > SORT_CAP) return false;
 
-    if (threadIdx.x == 0) s_n = 0;
-    __syncthreads();
-    for (int c = 0; c < NC; ++c) {
-        const int cnt = (int)counts[c];
-        const uint32_t* gsk = p.cand_sk + (slot0 + c) * CHUNK_CAP;
-        const uint32_t* gidx = p.cand_idx + (slot0 + c) * CHUNK_CAP;
-        for (int j0 = 0; j0 < cnt; j0 += NT) {
-            const int j = j0 + threadIdx.x;
-            uint32_t s = 0;
-            bool keep = false;
-            if (j < cnt) {
-                s = in_lds ? ck[off[c] + j] : gsk[j];
-                keep = s >= theta;
-            }
-            u64 mask = __ballot(keep);
-            if (mask) {
-                int first = __builtin_ctzll(mask);
-                uint32_t base = 0;
-                if (lane_id() == first) base = atomicAdd(&s_n, (uint32_t)__builtin_popcountll(mask));
-                base = __shfl(base, first, 64);
-                if (keep) {
-                    const uint32_t idx = gidx[j];
-                    const uint32_t vk = vkey(sel_inv(s, neg) / T);
-                    keys[base + lanes_below(mask)] = ((u64)vk << 32) | (u64)(0xFFFFFFFFu - idx);
-                }
+    // survivors -> sort keys (value key, ~index); their ids come in batches
+    for (int j0 = ml; j0 < mcnt; j0 += BATCH * tpc) {
+        uint32_t sv[BATCH], iv[BATCH];
+#pragma unroll
+        for (int b = 0; b < BATCH; ++b) {
+            const int j = j0 + b * tpc;
+            sv[b] = j < mcnt ? key_at(j) : 0u;
+            iv[b] = (j < mcnt && sv[b] >= theta) ? gidx[j] : 0u;
+        }
+#pragma unroll
+        for (int b = 0; b < BATCH; ++b) {
+            const int j = j0 + b * tpc;
+            if (j < mcnt && sv[b] >= theta) {
+                const uint32_t vk = vkey(sel_inv(sv[b], neg) / T);
+                keys[o++] = ((u64)vk << 32) | (u64)(0xFFFFFFFFu - iv[b]);
             }
         }
     }
@@ -717,14 +901,14 @@ __global__ __launch_bounds__(NT, 1) void k_rows(Params p)
         ChunkOut o = p.parts[(size_t)r * NC + c];
         best = o.best > best ? o.best : best;
         fl |= o.flags;
-        s_counts[c] = o.count;
+        s_counts[c] = o.count;   // raw candidates | history candidates << 16
     }
     best = block_max<u64>(best);
     const uint32_t flags = block_max<uint32_t>(fl & FLAG_BAD_HISTORY) |
-                           block_max<uint32_t>(fl & FLAG_OVERFLOW);
+                           block_max<uint32_t>(fl & FLAG_OVERFLOW) | block_max<uint32_t>(fl & FLAG_NAN);
     if (tid == 0) {
         uint32_t a = 0;
-        for (int c = 0; c < NC; ++c) { off[c] = a; a += s_counts[c]; }
+        for (int c = 0; c < NC; ++c) { off[c] = a; a += (s_counts[c] & 0xFFFFu) + (s_counts[c] >> 16); }
         off[NC] = a;
     }
     __syncthreads();
@@ -738,13 +922,15 @@ __global__ __launch_bounds__(NT, 1) void k_rows(Params p)
         st = MXS_ROW_BAD_HISTORY;
     } else if (mode == MODE_INVALID) {
         st = MXS_ROW_BAD_PARAM;
+    } else if (mode != MODE_GREEDY && (flags & FLAG_NAN)) {
+        st = MXS_ROW_NONFINITE;    // a NaN logit: no finite maximum (sampling.py:58/68 give NaN)
     } else if (mode == MODE_GREEDY) {
         tok = (int64_t)(0xFFFFFFFFu - (uint32_t)best);
         if (p.out_probs && tid == 0) p.out_probs[(size_t)r * (size_t)V + (size_t)tok] = 1.0f;
     } else {
         bool done = false;
         if (mode == MODE_TOPK && !(flags & FLAG_OVERFLOW))
-            done = finish_topk(p, r, T, k, top_p, u, s_counts, off, N, tok, st);
+            done = finish_topk(p, r, T, k, top_p, pen, u, s_counts, off, N, tok, st);
         if (!done) {
             __syncthreads();
             finish_large<TIn>(p, r, T, k, top_p, pen, pen_on, best, u, tok, st);
