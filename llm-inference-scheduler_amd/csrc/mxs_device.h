@@ -29,8 +29,8 @@ constexpr int MASS_SHIFT = 20;          // masses carry 44 fractional bits: 24-b
 constexpr uint32_t SK_MIN = 0x007FFFFFu;  // selection key of -inf (T > 0) or +inf (T < 0)
 
 // LDS map of the chunk kernel (dynamic shared memory).
-constexpr int K1_KS = 0;                        // 4 * NT group-extreme keys
-constexpr int K1_HIST = K1_KS + 16 * NT;        // 2048 x u32 histogram
+constexpr int K1_KS = 0;                        // 8 * NT group-extreme keys
+constexpr int K1_HIST = K1_KS + 32 * NT;        // 2048 x u32 histogram
 constexpr int K1_BM = K1_HIST + 8192;           // CS_MAX bits of history bitmap
 constexpr int K1_LDS_BYTES = K1_BM + CS_MAX / 8;
 

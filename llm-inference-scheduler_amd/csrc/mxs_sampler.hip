@@ -137,7 +137,7 @@ __device__ __forceinline__ float penalize(float v, float pen) { return v > 0.0f 
 // >= fl32(x(th) / T).  Division by T is monotone, so the predicate is
 // monotone in s; values a few ulps below x(th) can round onto the same
 // tempered value and then tie with it.
-__device__ uint32_t widen_threshold(uint32_t th, float T, bool neg)
+__device__ __forceinline__ uint32_t widen_threshold(uint32_t th, float T, bool neg)
 {
     __shared__ uint32_t s_res;
     if (wave_id() == 0) {
@@ -177,7 +177,7 @@ struct Reduced {
 };
 
 // One barrier round: max of a, min of b, OR of c over the workgroup.
-__device__ Reduced block_reduce(uint32_t a, uint32_t b, uint32_t c)
+__device__ __forceinline__ Reduced block_reduce(uint32_t a, uint32_t b, uint32_t c)
 {
     __shared__ uint32_t s[3][NWAVES];
     for (int o = 32; o > 0; o >>= 1) {
@@ -199,10 +199,11 @@ __device__ Reduced block_reduce(uint32_t a, uint32_t b, uint32_t c)
     return r;
 }
 
-// The r-th largest (0-based) of the cb <= 64 keys of ks[0 .. 4*NT) that fall
+// The r-th largest (0-based) of the cb <= 64 keys of ks[0 .. G*NT) that fall
 // in histogram bin `bin` ((key - lo) >> sh == bin): gathered into one wave and
 // ranked by shuffles.  `fallback` is returned if the gather disagrees.
-__device__ uint32_t exact_in_bin(const uint32_t* ks, uint32_t lo, int sh, uint32_t bin, uint32_t cb,
+template <int G>
+__device__ __forceinline__ uint32_t exact_in_bin(const uint32_t* ks, uint32_t lo, int sh, uint32_t bin, uint32_t cb,
                                  uint32_t r, uint32_t fallback)
 {
     __shared__ uint32_t s_keys[64];
@@ -210,9 +211,9 @@ __device__ uint32_t exact_in_bin(const uint32_t* ks, uint32_t lo, int sh, uint32
     if (threadIdx.x == 0) { s_n = 0; s_res = fallback; }
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t key = ks[4 * threadIdx.x + i];
-        if (((key - lo) >> sh) == bin) {
+    for (int i = 0; i < G; ++i) {
+        const uint32_t key = ks[G * threadIdx.x + i];
+        if (key >= lo && ((key - lo) >> sh) == bin) {
             const uint32_t o = atomicAdd(&s_n, 1u);
             if (o < 64u) s_keys[o] = key;
         }
@@ -222,8 +223,8 @@ __device__ uint32_t exact_in_bin(const uint32_t* ks, uint32_t lo, int sh, uint32
         const uint32_t lane = (uint32_t)lane_id();
         const uint32_t mine = lane < cb ? s_keys[lane] : 0u;
         uint32_t gt = 0, ge = 0;
-        for (uint32_t t = 0; t < cb; ++t) {
-            const uint32_t o = __shfl(mine, (int)t, 64);
+        for (uint32_t t = 0; t < cb; ++t) {   // broadcast reads of the gathered keys
+            const uint32_t o = s_keys[t];
             gt += o > mine ? 1u : 0u;
             ge += o >= mine ? 1u : 0u;
         }
@@ -374,24 +375,31 @@ __global__ __launch_bounds__(NT, 2) void k_chunks(Params p)
             for (int i = 0; i < EPT; ++i) nan_any |= (x[i] != x[i]) ? 1u : 0u;
         }
 
-        // The extreme of each group of 8 logits in the order of x / T
+        // The extreme of each group of GS logits in the order of x / T
         // (max for T > 0, min for T < 0); NaNs never win.
-        constexpr int G = EPT / 8;
+        constexpr int GS = 4;
+        constexpr int G = EPT / GS;
+        // element x[GS*i] sits at local index group_start(i); ceil(n / GS)
+        // groups of the chunk hold at least one element
+        auto group_start = [&](int i) { return local((GS * i) / VW, (GS * i) % VW); };
+        const uint32_t groups = (uint32_t)(n + GS - 1) / GS;
         uint32_t gk[G];
         uint32_t gmax = 0, gmin = 0xFFFFFFFFu;
 #pragma unroll
         for (int i = 0; i < G; ++i) {
-            float a = x[8 * i];
+            float a = x[GS * i];
             if (!neg) {
 #pragma unroll
-                for (int q = 1; q < 8; ++q) a = fmaxf(a, x[8 * i + q]);
+                for (int q = 1; q < GS; ++q) a = fmaxf(a, x[GS * i + q]);
             } else {
 #pragma unroll
-                for (int q = 1; q < 8; ++q) a = fminf(a, x[8 * i + q]);
+                for (int q = 1; q < GS; ++q) a = fminf(a, x[GS * i + q]);
             }
-            gk[i] = (a != a) ? SK_MIN : selkey(a, neg);
+            // a group of padding only holds no element: key 0, left out below
+            const bool valid = group_start(i) < n;
+            gk[i] = !valid ? 0u : ((a != a) ? SK_MIN : selkey(a, neg));
             gmax = gk[i] > gmax ? gk[i] : gmax;
-            gmin = gk[i] < gmin ? gk[i] : gmin;
+            if (valid) gmin = gk[i] < gmin ? gk[i] : gmin;
         }
         const Reduced rd = block_reduce(gmax, gmin, nan_any);
         if (rd.any) flags |= FLAG_NAN;
@@ -400,7 +408,7 @@ __global__ __launch_bounds__(NT, 2) void k_chunks(Params p)
         if (mode == MODE_TOPK) {
             // sampling.py:52-54.  The group extremes are values of distinct
             // elements, so with k' = k + (history ids in the chunk) the k'-th
-            // largest of these 4*NT keys bounds the chunk's k'-th largest raw
+            // largest of these G*NT keys bounds the chunk's k'-th largest raw
             // key from below, and every element of the penalized top-k is a
             // history id or at least that large.  Candidates: raw keys at or
             // above the bound (widened over the rounding of x / T); then every
@@ -408,7 +416,7 @@ __global__ __launch_bounds__(NT, 2) void k_chunks(Params p)
             // row kernel penalizes.
             const uint32_t kp = (uint32_t)k + hc;
             uint32_t theta = 0;
-            if ((uint32_t)n > kp && kp <= (uint32_t)(G * NT)) {
+            if ((uint32_t)n > kp && kp <= groups) {
 #pragma unroll
                 for (int i = 0; i < G; ++i) ks[G * tid + i] = gk[i];
                 const uint32_t lo = rd.min;
@@ -417,13 +425,14 @@ __global__ __launch_bounds__(NT, 2) void k_chunks(Params p)
                 for (int b = tid; b < 2048; b += NT) hist[b] = 0;
                 __syncthreads();
 #pragma unroll
-                for (int i = 0; i < G; ++i) atomicAdd(&hist[(gk[i] - lo) >> sh], 1u);
+                for (int i = 0; i < G; ++i)
+                    if (gk[i] >= lo) atomicAdd(&hist[(gk[i] - lo) >> sh], 1u);
                 __syncthreads();
                 const BinHit hit = find_desc<uint32_t>(hist, 2048, (u64)(kp - 1u));
                 uint32_t th = lo + ((uint32_t)hit.bin << sh);   // the bin's lower edge bounds it
                 const uint32_t cb = hist[hit.bin];
                 if (sh > 0 && cb <= 64u)                           // exact: rank the bin's keys
-                    th = exact_in_bin(ks, lo, sh, (uint32_t)hit.bin, cb, kp - 1u - (uint32_t)hit.above, th);
+                    th = exact_in_bin<G>(ks, lo, sh, (uint32_t)hit.bin, cb, kp - 1u - (uint32_t)hit.above, th);
                 if (th < SK_MIN) th = SK_MIN;
                 theta = widen_threshold(th, T, neg);
             }
@@ -639,7 +648,7 @@ struct LargeRow {
 };
 
 template <typename TIn>
-__device__ void finish_large(const Params& p, int r, float T, int k, float top_p, float pen,
+__device__ __forceinline__ void finish_large(const Params& p, int r, float T, int k, float top_p, float pen,
                              bool pen_on, u64 best, float u, int64_t& tok, int32_t& st)
 {
     extern __shared__ __align__(16) unsigned char smem[];
@@ -724,6 +733,242 @@ __device__ void finish_large(const Params& p, int r, float T, int k, float top_p
     }
 }
 
+// The r-th largest (0-based) of the keys whose value lies in [blo, bhi],
+// known to number cnt <= 64: gathered into wave 0 and ranked by shuffles.
+template <class Visit>
+__device__ __forceinline__ uint32_t rank_in_range(Visit visit, uint32_t blo, uint32_t bhi, uint32_t cnt, uint32_t r)
+{
+    __shared__ uint32_t g_keys[64];
+    __shared__ uint32_t g_n, g_res;
+    if (threadIdx.x == 0) { g_n = 0; g_res = blo; }
+    __syncthreads();
+    visit([&](uint32_t k) {
+        if (k >= blo && k <= bhi) {
+            const uint32_t slot = atomicAdd(&g_n, 1u);
+            if (slot < 64u) g_keys[slot] = k;
+        }
+    });
+    __syncthreads();
+    if (wave_id() == 0) {
+        const uint32_t lane = (uint32_t)lane_id();
+        const uint32_t n = g_n < cnt ? g_n : cnt;
+        const uint32_t mine = lane < n ? g_keys[lane] : 0u;
+        uint32_t gt = 0, ge = 0;
+        for (uint32_t t = 0; t < n; ++t) {   // broadcast reads of the gathered keys
+            const uint32_t other = g_keys[t];
+            gt += other > mine ? 1u : 0u;
+            ge += other >= mine ? 1u : 0u;
+        }
+        const u64 mask = __ballot(lane < n && gt <= r && r < ge);
+        if (mask && lane == (uint32_t)__builtin_ctzll(mask)) g_res = mine;
+    }
+    __syncthreads();
+    const uint32_t res = g_res;
+    __syncthreads();
+    return res;
+}
+
+// Exact kk-th largest (1-based) key.  Each level histograms the keys of the
+// current range into 2048 bins spanning exactly that range; a bin of at most
+// 64 keys is finished by ranking, otherwise it becomes the next range.
+template <class Visit>
+__device__ __forceinline__ uint32_t select_exact(uint32_t kk, Visit visit, uint32_t* hist)
+{
+    uint32_t mx = 0, mn = 0xFFFFFFFFu;
+    visit([&](uint32_t k) { mx = k > mx ? k : mx; mn = k < mn ? k : mn; });
+    const Reduced rd = block_reduce(mx, mn, 0u);
+    uint32_t lo = rd.min, hi = rd.max;
+    for (int lev = 0; lev < 4 && lo != hi; ++lev) {
+        const uint32_t span = hi - lo;
+        const int sh = span >= 2048u ? (32 - __builtin_clz(span)) - 11 : 0;
+        for (int b = threadIdx.x; b < 2048; b += NT) hist[b] = 0;
+        __syncthreads();
+        visit([&](uint32_t k) {
+            if (k >= lo && k <= hi) atomicAdd(&hist[(k - lo) >> sh], 1u);
+        });
+        __syncthreads();
+        const BinHit hit = find_desc<uint32_t>(hist, 2048, (u64)(kk - 1u));
+        const uint32_t cnt = hist[hit.bin];
+        const uint32_t blo = lo + ((uint32_t)hit.bin << sh);
+        const u64 top = (u64)blo + ((u64)1 << sh) - 1;
+        const uint32_t bhi = top < (u64)hi ? (uint32_t)top : hi;
+        kk -= (uint32_t)hit.above;
+        __syncthreads();
+        if (sh == 0) return blo;
+        if (cnt <= 64u) return rank_in_range(visit, blo, bhi, cnt, kk - 1u);
+        lo = blo;
+        hi = bhi;
+    }
+    return lo;
+}
+
+// Fallback of finish_kept for heavy ties: bitonic sort of the kept set, then
+// the prefix sums in sorted order.
+__device__ __forceinline__ bool finish_sorted(const Params& p, int r, u64* keys, u64* cum, int n1, float top_p, float u,
+                              int64_t& tok, int32_t& st)
+{
+    __syncthreads();
+    const int P = pow2_ceil(n1);
+    for (int j = n1 + threadIdx.x; j < P; j += NT) keys[j] = 0;
+    __syncthreads();
+    bitonic_sort_desc(keys, P);
+    const float m = okey_inv((uint32_t)(keys[0] >> 32));
+    if (!isfinite(m)) { st = MXS_ROW_NONFINITE; tok = -1; return true; }
+    constexpr int PER = SORT_CAP / NT;
+    const int j0 = threadIdx.x * PER;
+    u64 wv[PER], run = 0;
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+        int j = j0 + q;
+        u64 w = 0;
+        if (j < n1) w = mass_of(okey_inv((uint32_t)(keys[j] >> 32)) - m);
+        wv[q] = w;
+        run += w;
+    }
+    u64 W;
+    u64 acc = block_incl_scan<u64>(run, &W) - run;
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+        acc += wv[q];
+        cum[j0 + q] = acc;
+    }
+    __syncthreads();
+    int nstar = n1;
+    if (top_p < 1.0f) {
+        if (!(top_p > 0.0f)) { st = MXS_ROW_EMPTY_NUCLEUS; tok = -1; return true; }
+        const u64 Tm = ceil_mul(top_p, W);
+        uint32_t cnt = 0;
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            int j = j0 + q;
+            if (j < n1 && cum[j] - wv[q] < Tm) ++cnt;
+        }
+        nstar = (int)block_sum<uint32_t>(cnt);
+    }
+    const u64 Wk = cum[nstar - 1];
+    const u64 D = floor_mul(clamp_uniform(u), Wk);
+    uint32_t below = 0;
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+        int j = j0 + q;
+        if (j < nstar && cum[j] <= D) ++below;
+    }
+    const int jd = (int)block_sum<uint32_t>(below);
+    tok = (int64_t)(0xFFFFFFFFu - (uint32_t)keys[jd]);
+    st = MXS_ROW_OK;
+    if (p.out_probs) {
+        float* out = p.out_probs + (size_t)r * (size_t)p.V;
+        for (int j = threadIdx.x; j < nstar; j += NT) {
+            u64 w = cum[j] - (j ? cum[j - 1] : 0ull);
+            out[0xFFFFFFFFu - (uint32_t)keys[j]] = (float)((double)w / (double)Wk);
+        }
+    }
+    return true;
+}
+
+struct Picked {
+    u64 key;   // (value key << 32) | ~index
+    u64 E;     // mass before it in sorted order
+    u64 w;     // its mass
+    int ok;    // 0: the bin held more than 64 elements
+};
+
+// Kept-by-top-k tokens in LDS (keys[0..n) as (value key << 32 | ~index), any
+// order) -> top-p cut, draw and post-filter probabilities (sampling.py:56-69).
+// Masses go into a histogram over value bins; the bin holding a given mass
+// position is finished by ranking its elements in one wave.  A bin of more
+// than 64 elements (heavy ties) falls back to a bitonic sort of the set.
+__device__ __forceinline__ bool finish_kept(const Params& p, int r, u64* keys, u64* wm, int n, float top_p, float u,
+                            int64_t& tok, int32_t& st)
+{
+    extern __shared__ __align__(16) unsigned char smem[];
+    u64* MH = (u64*)(smem + K2_A);
+    uint32_t* CH = (uint32_t*)(smem + K2_HIST);
+    __shared__ u64 g_key[64], g_w[64];
+    __shared__ uint32_t g_n;
+    __shared__ Picked g_pick;
+
+    uint32_t vmax = 0, vmin = 0xFFFFFFFFu;
+    for (int j = threadIdx.x; j < n; j += NT) {
+        const uint32_t vk = (uint32_t)(keys[j] >> 32);
+        vmax = vk > vmax ? vk : vmax;
+        vmin = vk < vmin ? vk : vmin;
+    }
+    const Reduced rd = block_reduce(vmax, vmin, 0u);
+    const float m = okey_inv(rd.max);
+    if (!isfinite(m)) { st = MXS_ROW_NONFINITE; tok = -1; return true; }
+    const uint32_t span = rd.max - rd.min;
+    const int sh = span >= 2048u ? (32 - __builtin_clz(span)) - 11 : 0;
+    for (int b = threadIdx.x; b < 2048; b += NT) { MH[b] = 0; CH[b] = 0; }
+    __syncthreads();
+    u64 part = 0;
+    for (int j = threadIdx.x; j < n; j += NT) {
+        const uint32_t vk = (uint32_t)(keys[j] >> 32);
+        const u64 w = mass_of(okey_inv(vk) - m);
+        wm[j] = w;
+        part += w;
+        const uint32_t bin = (vk - rd.min) >> sh;
+        atomicAdd(&MH[bin], w);
+        atomicAdd(&CH[bin], 1u);
+    }
+    const u64 W = block_sum<u64>(part);
+
+    // the element at mass position t of the sorted order (value desc, index asc)
+    auto pick = [&](u64 t) -> Picked {
+        const BinHit hit = find_desc<u64>(MH, 2048, t);
+        const uint32_t cnt = CH[hit.bin];
+        if (threadIdx.x == 0) { g_n = 0; g_pick = Picked{0, 0, 0, cnt <= 64u ? 1 : 0}; }
+        __syncthreads();
+        if (cnt <= 64u) {
+            for (int j = threadIdx.x; j < n; j += NT) {
+                if ((((uint32_t)(keys[j] >> 32) - rd.min) >> sh) == (uint32_t)hit.bin) {
+                    const uint32_t slot = atomicAdd(&g_n, 1u);
+                    if (slot < 64u) { g_key[slot] = keys[j]; g_w[slot] = wm[j]; }
+                }
+            }
+            __syncthreads();
+            if (wave_id() == 0) {
+                const uint32_t lane = (uint32_t)lane_id();
+                const uint32_t c = g_n < 64u ? g_n : 64u;
+                const u64 mk = lane < c ? g_key[lane] : 0ull;
+                const u64 mw = lane < c ? g_w[lane] : 0ull;
+                u64 before = 0;
+                for (uint32_t q = 0; q < c; ++q)   // broadcast reads of the gathered bin
+                    before += g_key[q] > mk ? g_w[q] : 0ull;
+                const u64 E = hit.above + before;
+                if (lane < c && E <= t && t < E + mw) g_pick = Picked{mk, E, mw, 1};
+            }
+        }
+        __syncthreads();
+        const Picked res = g_pick;
+        __syncthreads();
+        return res;
+    };
+
+    bool bounded = false;
+    u64 bound = 0, Wk = W;
+    if (top_p < 1.0f) {   // sampling.py:56-63
+        if (!(top_p > 0.0f)) { st = MXS_ROW_EMPTY_NUCLEUS; tok = -1; return true; }
+        const Picked b = pick(ceil_mul(top_p, W) - 1);
+        if (!b.ok) return finish_sorted(p, r, keys, wm, n, top_p, u, tok, st);
+        bounded = true;
+        bound = b.key;
+        Wk = b.E + b.w;
+    }
+    const Picked d = pick(floor_mul(clamp_uniform(u), Wk));   // sampling.py:69
+    if (!d.ok) return finish_sorted(p, r, keys, wm, n, top_p, u, tok, st);
+    tok = (int64_t)(0xFFFFFFFFu - (uint32_t)d.key);
+    st = MXS_ROW_OK;
+
+    if (p.out_probs) {   // sampling.py:68
+        float* out = p.out_probs + (size_t)r * (size_t)p.V;
+        for (int j = threadIdx.x; j < n; j += NT)
+            if (!bounded || keys[j] >= bound)
+                out[0xFFFFFFFFu - (uint32_t)keys[j]] = (float)((double)wm[j] / (double)Wk);
+    }
+    return true;
+}
+
 // Top-k rows.  The chunks' candidates hold every element whose tempered
 // value reaches the row's k-th largest.  Returns false when the survivors do
 // not fit the LDS sort; the caller then takes the multi-pass path.
@@ -731,8 +976,9 @@ __device__ void finish_large(const Params& p, int r, float T, int k, float top_p
 // Each thread owns a slice of one chunk's candidate slot (NT / NC threads per
 // chunk) and moves it in unrolled batches, so a batch costs one memory round
 // trip rather than one per element.
-__device__ bool finish_topk(const Params& p, int r, float T, int k, float top_p, float pen, float u,
-                            const uint32_t* counts, const uint32_t* off, int N,
+template <bool IN_LDS>
+__device__ __forceinline__ bool finish_topk(const Params& p, int r, float T, int k, float top_p, float pen, float u,
+                            const uint32_t* counts, const uint32_t* off,
                             int64_t& tok, int32_t& st)
 {
     extern __shared__ __align__(16) unsigned char smem[];
@@ -756,10 +1002,9 @@ __device__ bool finish_topk(const Params& p, int r, float T, int k, float top_p,
     const size_t mslot = ((size_t)r * NC + (active ? mc : 0)) * CHUNK_CAP;
     const uint32_t* gsk = p.cand_sk + mslot;
     const uint32_t* gidx = p.cand_idx + mslot;
-    const bool in_lds = N <= CAND_LDS;
     uint32_t* mck = ck + (active ? off[mc] : 0);
 
-    if (in_lds) {
+    if (IN_LDS) {
         for (int j0 = ml; j0 < mcnt; j0 += BATCH * tpc) {
             uint32_t v[BATCH];
 #pragma unroll
@@ -776,14 +1021,15 @@ __device__ bool finish_topk(const Params& p, int r, float T, int k, float top_p,
         __syncthreads();
     }
     auto key_at = [&](int j) -> uint32_t {
-        return in_lds ? mck[j] : (j < mc1 ? gsk[j] : penalized(gsk[j]));
+        if (IN_LDS) return mck[j];
+        return j < mc1 ? gsk[j] : penalized(gsk[j]);
     };
     auto visit = [&](auto&& f) {
         for (int j = ml; j < mcnt; j += tpc) f(key_at(j));
     };
 
     // sampling.py:52-54: the k-th largest, then everything that rounds onto it
-    uint32_t sk_k = block_select_desc_v(kk, visit, hist, 0u);
+    uint32_t sk_k = select_exact(kk, visit, hist);
     if (sk_k < SK_MIN) sk_k = SK_MIN;
     const uint32_t theta = widen_threshold(sk_k, T, neg);
     uint32_t mine = 0;
@@ -793,14 +1039,15 @@ __device__ bool finish_topk(const Params& p, int r, float T, int k, float top_p,
     const int n1 = (int)n1u;
     if (n1 > SORT_CAP) return false;
 
-    // survivors -> sort keys (value key, ~index); their ids come in batches
+    // survivors -> (value key << 32 | ~index); their ids come in batches
     for (int j0 = ml; j0 < mcnt; j0 += BATCH * tpc) {
         uint32_t sv[BATCH], iv[BATCH];
 #pragma unroll
-        for (int b = 0; b < BATCH; ++b) {
+        for (int b = 0; b < BATCH; ++b) {   // every load of the batch in flight at once
             const int j = j0 + b * tpc;
+            const int jc = j < mcnt ? j : 0;
             sv[b] = j < mcnt ? key_at(j) : 0u;
-            iv[b] = (j < mcnt && sv[b] >= theta) ? gidx[j] : 0u;
+            iv[b] = gidx[jc];
         }
 #pragma unroll
         for (int b = 0; b < BATCH; ++b) {
@@ -812,70 +1059,7 @@ __device__ bool finish_topk(const Params& p, int r, float T, int k, float top_p,
         }
     }
     __syncthreads();
-    const int P = pow2_ceil(n1);
-    for (int j = n1 + threadIdx.x; j < P; j += NT) keys[j] = 0;
-    __syncthreads();
-    bitonic_sort_desc(keys, P);
-
-    // sampling.py:57-59: masses in sorted order and their inclusive prefix sums
-    const float m = okey_inv((uint32_t)(keys[0] >> 32));
-    if (!isfinite(m)) { st = MXS_ROW_NONFINITE; tok = -1; return true; }
-    constexpr int PER = SORT_CAP / NT;
-    const int j0 = threadIdx.x * PER;
-    u64 wv[PER], run = 0;
-#pragma unroll
-    for (int q = 0; q < PER; ++q) {
-        int j = j0 + q;
-        u64 w = 0;
-        if (j < n1) w = mass_of(okey_inv((uint32_t)(keys[j] >> 32)) - m);
-        wv[q] = w;
-        run += w;
-    }
-    u64 W;
-    u64 acc = block_incl_scan<u64>(run, &W) - run;
-#pragma unroll
-    for (int q = 0; q < PER; ++q) {
-        acc += wv[q];
-        cum[j0 + q] = acc;
-    }
-    __syncthreads();
-
-    // sampling.py:56, 62-63: keep j while the mass before it is < top_p * W
-    int nstar = n1;
-    if (top_p < 1.0f) {
-        if (!(top_p > 0.0f)) { st = MXS_ROW_EMPTY_NUCLEUS; tok = -1; return true; }
-        const u64 Tm = ceil_mul(top_p, W);
-        uint32_t cnt = 0;
-#pragma unroll
-        for (int q = 0; q < PER; ++q) {
-            int j = j0 + q;
-            if (j < n1 && cum[j] - wv[q] < Tm) ++cnt;
-        }
-        nstar = (int)block_sum<uint32_t>(cnt);
-    }
-    const u64 Wk = cum[nstar - 1];
-
-    // sampling.py:69: the first j with C_j > floor(u * Wk)
-    const u64 D = floor_mul(clamp_uniform(u), Wk);
-    uint32_t below = 0;
-#pragma unroll
-    for (int q = 0; q < PER; ++q) {
-        int j = j0 + q;
-        if (j < nstar && cum[j] <= D) ++below;
-    }
-    const int jd = (int)block_sum<uint32_t>(below);
-    tok = (int64_t)(0xFFFFFFFFu - (uint32_t)keys[jd]);
-    st = MXS_ROW_OK;
-
-    // sampling.py:68
-    if (p.out_probs) {
-        float* out = p.out_probs + (size_t)r * (size_t)V;
-        for (int j = threadIdx.x; j < nstar; j += NT) {
-            u64 w = cum[j] - (j ? cum[j - 1] : 0ull);
-            out[0xFFFFFFFFu - (uint32_t)keys[j]] = (float)((double)w / (double)Wk);
-        }
-    }
-    return true;
+    return finish_kept(p, r, keys, cum, n1, top_p, u, tok, st);
 }
 
 template <typename TIn>
@@ -930,7 +1114,8 @@ __global__ __launch_bounds__(NT, 1) void k_rows(Params p)
     } else {
         bool done = false;
         if (mode == MODE_TOPK && !(flags & FLAG_OVERFLOW))
-            done = finish_topk(p, r, T, k, top_p, pen, u, s_counts, off, N, tok, st);
+            done = N <= CAND_LDS ? finish_topk<true>(p, r, T, k, top_p, pen, u, s_counts, off, tok, st)
+                                 : finish_topk<false>(p, r, T, k, top_p, pen, u, s_counts, off, tok, st);
         if (!done) {
             __syncthreads();
             finish_large<TIn>(p, r, T, k, top_p, pen, pen_on, best, u, tok, st);
