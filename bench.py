@@ -85,14 +85,41 @@ def time_cpu_baseline(w, budget_s: float, max_rows: int):
     }
 
 
-def load_traffic(workload: str):
-    """HBM bytes per launch from the committed rocprofv3 counter summary."""
-    path = os.path.join(ROOT, "profiles", f"traffic_{workload}.json")
+def load_traffic(workload: str, B: int):
+    """HBM bytes per call from the committed rocprofv3 counter summary
+    (FETCH_SIZE and WRITE_SIZE, each scaled by a plain copy's reading)."""
+    path = os.path.join(ROOT, "profiles", f"{workload}_B{B}_hbm_traffic.md")
     try:
         with open(path) as f:
-            return json.load(f).get("hbm_bytes_per_launch")
+            for line in f:
+                if line.startswith("hbm_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
     except (OSError, ValueError):
-        return None
+        pass
+    return None
+
+
+def copy_calibration(dev, nbytes: int, steps: int, warmup: int):
+    """A plain device-to-device copy of `nbytes`: it reads and writes exactly
+    nbytes each, so HBM byte counters read over it give their scale factor."""
+    import numpy as np
+    import torch
+    src = torch.ones(nbytes // 4, dtype=torch.int32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(warmup):
+        dst.copy_(src)
+    stream = torch.cuda.current_stream(dev)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
+    for a, b in evs:
+        a.record(stream)
+        dst.copy_(src)
+        b.record(stream)
+    torch.cuda.synchronize()
+    us = np.array([a.elapsed_time(b) * 1e3 for a, b in evs])
+    print(json.dumps({"copy_bytes": src.numel() * 4, "steps": steps, "kernel_us_mean": float(us.mean()),
+                      "gbps_read_plus_write": 2 * src.numel() * 4 / (us.mean() * 1e-6) / 1e9}),
+          flush=True)
 
 
 def main():
@@ -107,6 +134,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
     ap.add_argument("--cold", action="store_true", help="also time with the MALL flushed")
+    ap.add_argument("--copy-bytes", type=int, default=0,
+                    help="instead of the sampler, time a plain device copy of this many bytes "
+                         "(the reference point for HBM byte counters)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -123,6 +153,9 @@ def main():
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.copy_bytes:
+        copy_calibration(dev, args.copy_bytes, args.steps, args.warmup)
+        return
     log(f"[bench] building workload {args.workload}")
     w = make_workload(args.workload, B=args.batch)
     d = w.to_device(dev)
@@ -186,7 +219,7 @@ def main():
     achieved = algo / (mean_us * 1e-6) / 1e9
     rows_per_s = w.B / (ms_per_step * 1e-3)
     dtype = "fp16->fp32" if w.logits.dtype == np.float16 else "fp32"
-    traffic = load_traffic(args.workload) if args.batch is None else None
+    traffic = load_traffic(args.workload, w.B)
     out = {
         "metric": METRIC,
         "value": rows_per_s,
@@ -218,7 +251,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
                      "algorithmic_bytes_per_launch": algo,
-                     "kernel": "k_sample (one launch per batch)"},
+                     "kernel": "mxs_sample call: k_chunks + k_rows on one stream"},
         "cold_mall": cold,
         "parity_vs_oracle": parity,
     }
