@@ -51,7 +51,7 @@ enum mxs_row_status {
     MXS_ROW_OK = 0,
     MXS_ROW_BAD_HISTORY = 1,    /* a history id is outside [0, V) (torch: IndexError) */
     MXS_ROW_BAD_PARAM = 2,      /* temperature is NaN */
-    MXS_ROW_NONFINITE = 3,      /* max tempered logit is inf/NaN (torch: multinomial error) */
+    MXS_ROW_NONFINITE = 3,      /* a tempered logit is NaN or the max is infinite (torch: multinomial error) */
     MXS_ROW_EMPTY_NUCLEUS = 4   /* top_p <= 0 removes every token (torch: multinomial error) */
 };
 

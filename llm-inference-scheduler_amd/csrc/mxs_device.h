@@ -41,14 +41,27 @@ constexpr int K2_HIST = K2_B + 65536;           // 2048 x u32
 constexpr int K2_OFF = K2_HIST + 8192;          // NC_MAX + 1 candidate offsets
 constexpr int K2_LDS_BYTES = K2_OFF + 4 * (NC_MAX + 1);
 
+// LDS map of the one-workgroup-per-row kernel.
+constexpr int FCAP = 12288;                     // candidates held while streaming
+constexpr int FTILE = 8192;                     // logits streamed between capacity checks
+constexpr int FSEG = FCAP / NWAVES;             // buffer segment of one wave
+constexpr int NSAMP = 2048;                     // logits sampled for the first bound
+constexpr int FAST_MIN_V = 8 * NSAMP;           // rows shorter than this skip the sample
+constexpr int KF_CK = 0;                        // FCAP candidate keys; later SORT_CAP masses
+constexpr int KF_CI = KF_CK + 4 * FCAP;         // FCAP candidate ids
+constexpr int KF_BM = KF_CI + 4 * FCAP;         // history bitmap (MXS_MAX_VOCAB bits); later sort keys
+constexpr int KF_MH = KF_BM + 32768;            // 2048 x u64
+constexpr int KF_H = KF_MH + 16384;             // 2048 x u32
+constexpr int KF_LDS_BYTES = KF_H + 8192;
+
 __host__ __device__ __forceinline__ uint32_t f2u(float f) { return __builtin_bit_cast(uint32_t, f); }
 __host__ __device__ __forceinline__ float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
 
 // Order-preserving key: a < b (non-NaN)  =>  okey(a) < okey(b).
 __host__ __device__ __forceinline__ uint32_t okey(float f)
 {
-    uint32_t u = f2u(f);
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    const uint32_t u = f2u(f);   // negative: all bits flipped; otherwise the sign bit set
+    return u ^ ((uint32_t)((int32_t)u >> 31) | 0x80000000u);
 }
 __host__ __device__ __forceinline__ float okey_inv(uint32_t k)
 {
@@ -60,8 +73,7 @@ __host__ __device__ __forceinline__ uint32_t vkey(float f) { return okey(f == 0.
 // Selection key of a penalized logit x: ordered like x / T (reversed for T < 0).
 __device__ __forceinline__ uint32_t selkey(float x, bool neg)
 {
-    uint32_t k = okey(x);
-    return neg ? ~k : k;
+    return okey(x) ^ (neg ? 0xFFFFFFFFu : 0u);
 }
 __device__ __forceinline__ float sel_inv(uint32_t s, bool neg) { return okey_inv(neg ? ~s : s); }
 

@@ -372,7 +372,10 @@ __global__ __launch_bounds__(NT, 2) void k_chunks(Params p)
         uint32_t nan_any = 0;
         if (!isfinite(acc)) {
 #pragma unroll
-            for (int i = 0; i < EPT; ++i) nan_any |= (x[i] != x[i]) ? 1u : 0u;
+            for (int i = 0; i < EPT; ++i) {   // NaN after x / T: a NaN, or infinity over infinity
+                const bool real = local(i / VW, i % VW) < n;   // (padding is infinite)
+                nan_any |= ((x[i] != x[i]) || (real && __builtin_isinf(T) && __builtin_isinf(x[i]))) ? 1u : 0u;
+            }
         }
 
         // The extreme of each group of GS logits in the order of x / T
@@ -647,11 +650,23 @@ struct LargeRow {
     }
 };
 
+// LDS regions the multi-pass path works in.
+struct LargeLds {
+    uint32_t* rbm;   // V bits: history bitmap of the row
+    u64* MH;         // 2048 masses
+    u64* keys;       // LCAP sort keys (may overlap MH)
+    uint32_t* CH;    // 2048 counts
+};
+
+// skmax: the row's largest selection key, over penalized values when
+// max_penalized (else over raw values, and it is taken again here).
+// thk_known: the top-k threshold thk is already exact (else it is selected).
 template <typename TIn>
 __device__ __forceinline__ void finish_large(const Params& p, int r, float T, int k, float top_p, float pen,
-                             bool pen_on, u64 best, float u, int64_t& tok, int32_t& st)
+                             bool pen_on, bool bitmap_ready, uint32_t skmax, bool max_penalized,
+                             bool thk_known, uint32_t thk, float u, const LargeLds& lds,
+                             int64_t& tok, int32_t& st)
 {
-    extern __shared__ __align__(16) unsigned char smem[];
     const int V = p.V;
     LargeRow<TIn> L;
     L.row = (const TIn*)p.logits + (size_t)r * (size_t)p.ld;
@@ -660,26 +675,24 @@ __device__ __forceinline__ void finish_large(const Params& p, int r, float T, in
     L.neg = T < 0.0f;
     L.pen = pen;
     L.pen_on = pen_on;
-    uint32_t* rbm = (uint32_t*)(smem + K2_A);
+    uint32_t* rbm = lds.rbm;
     L.rbm = rbm;
-    L.MH = (u64*)(smem + K2_B);
-    L.keys = (u64*)(smem + K2_B);
-    L.CH = (uint32_t*)(smem + K2_HIST);
+    L.MH = lds.MH;
+    L.keys = lds.keys;
+    L.CH = lds.CH;
 
-    if (pen_on) {
+    if (pen_on && !bitmap_ready) {
         const int words = (V + 31) >> 5;
         for (int w = threadIdx.x; w < words; w += NT) rbm[w] = 0;
         __syncthreads();
         for (int h = p.hoff[r] + threadIdx.x; h < p.hoff[r + 1]; h += NT) {
-            int id = p.hids[h];     // range-checked by k_chunks
+            int id = p.hids[h];     // range-checked before this point
             atomicOr(&rbm[id >> 5], 1u << (id & 31));
         }
         __syncthreads();
     }
 
-    // the chunks' maximum is over raw logits; with a penalty take it again
-    uint32_t skmax = (uint32_t)(best >> 32);
-    if (pen_on) {
+    if (pen_on && !max_penalized) {
         uint32_t mx = 0;
         for (int i = threadIdx.x; i < V; i += NT) {
             const uint32_t sk = selkey(L.x_at(i), L.neg);
@@ -692,8 +705,8 @@ __device__ __forceinline__ void finish_large(const Params& p, int r, float T, in
     L.m = m;
 
     // sampling.py:52-54: exact k-th largest over the row
-    L.thk = 0;
-    if (k > 0 && k < V) {
+    L.thk = thk_known ? thk : 0;
+    if (!thk_known && k > 0 && k < V) {
         auto key = [&](int i) -> uint32_t { return selkey(L.x_at(i), L.neg); };
         uint32_t skk = block_select_desc(V, (uint32_t)k, key, L.CH, 0u);
         if (skk < SK_MIN) skk = SK_MIN;
@@ -879,11 +892,8 @@ struct Picked {
 // position is finished by ranking its elements in one wave.  A bin of more
 // than 64 elements (heavy ties) falls back to a bitonic sort of the set.
 __device__ __forceinline__ bool finish_kept(const Params& p, int r, u64* keys, u64* wm, int n, float top_p, float u,
-                            int64_t& tok, int32_t& st)
+                            u64* MH, uint32_t* CH, int64_t& tok, int32_t& st)
 {
-    extern __shared__ __align__(16) unsigned char smem[];
-    u64* MH = (u64*)(smem + K2_A);
-    uint32_t* CH = (uint32_t*)(smem + K2_HIST);
     __shared__ u64 g_key[64], g_w[64];
     __shared__ uint32_t g_n;
     __shared__ Picked g_pick;
@@ -1059,7 +1069,7 @@ __device__ __forceinline__ bool finish_topk(const Params& p, int r, float T, int
         }
     }
     __syncthreads();
-    return finish_kept(p, r, keys, cum, n1, top_p, u, tok, st);
+    return finish_kept(p, r, keys, cum, n1, top_p, u, (u64*)(smem + K2_A), (uint32_t*)(smem + K2_HIST), tok, st);
 }
 
 template <typename TIn>
@@ -1118,7 +1128,485 @@ __global__ __launch_bounds__(NT, 1) void k_rows(Params p)
                                  : finish_topk<false>(p, r, T, k, top_p, pen, u, s_counts, off, tok, st);
         if (!done) {
             __syncthreads();
-            finish_large<TIn>(p, r, T, k, top_p, pen, pen_on, best, u, tok, st);
+            const LargeLds lds{(uint32_t*)(smem + K2_A), (u64*)(smem + K2_B), (u64*)(smem + K2_B),
+                               (uint32_t*)(smem + K2_HIST)};
+            finish_large<TIn>(p, r, T, k, top_p, pen, pen_on, false, (uint32_t)(best >> 32), false,
+                              false, 0u, u, lds, tok, st);
+        }
+    }
+    if (tid == 0) {
+        p.out_tok[r] = st == MXS_ROW_OK ? tok : -1;
+        if (p.out_status) p.out_status[r] = st;
+    }
+}
+
+// ================================================================ k_fused
+//
+// One workgroup per row, the whole chain in one launch.  The row streams from
+// HBM once, in 128-bit loads with two tiles of FTILE logits in flight per
+// workgroup; the penalty is applied from an LDS bitmap of the row's history.
+//   greedy  a packed (key, index) maximum;
+//   top-k   every element whose selection key reaches a running lower bound
+//           theta on the row's k-th largest key is kept in an LDS buffer.
+//           When the buffer nears capacity, theta rises to the lower edge of
+//           the histogram bin holding the k-th largest buffered key (k
+//           buffered elements are at least that large, so the bound stays
+//           valid), widened over the rounding of x / T, and the buffer is
+//           compacted.  The exact k-th key, the top-p cut and the draw then
+//           come from the buffer alone;
+//   other   the row's extreme keys, then the multi-pass path.
+
+// Streams the row in tiles of FTILE logits, FTILE / NT = 16 per thread:
+// elem(i, e, x) for slot i in [0, 16) of this thread's share of the tile,
+// element index e and its penalized value x; then tile_end(id), called by all
+// threads (it may synchronize), where id(i) is the element index of slot i in
+// that tile; it returns true to stop the stream.  Slot i of a tile is skipped
+// when it lies past the row's end.
+//
+// Whole tiles are loaded with unconditional 128-bit loads, alternating two
+// register buffers so that the next tile is in flight while this one is
+// processed (conditional loads would make the compiler wait for all of them).
+constexpr int FPT = FTILE / NT;   // logits per thread per tile (16)
+
+template <typename TIn, class Elem, class TileEnd>
+__device__ __forceinline__ void stream_row(const TIn* rowp, int V, const uint32_t* bm, bool pen_on, float pen,
+                                           Elem&& elem, TileEnd&& tile_end)
+{
+    typedef VecIO<TIn> IO;
+    constexpr int VW = IO::W;
+    constexpr int FU = FPT / VW;            // 16-byte loads per thread per tile
+    constexpr int TV = NT * FU;             // vectors per tile
+    typedef typename IO::vec_t vec_t;
+    const int tid = threadIdx.x;
+    const bool vec_ok = (((uintptr_t)rowp) & 15u) == 0;
+    const int nfull = vec_ok ? V / (TV * VW) : 0;   // tiles wholly inside the row
+    const vec_t* src = (const vec_t*)rowp;
+
+    auto load = [&](vec_t (&b)[FU], int t) {
+#pragma unroll
+        for (int j = 0; j < FU; ++j) b[j] = src[t * TV + j * NT + tid];
+    };
+    auto proc = [&](const vec_t (&b)[FU], int t) {
+        uint32_t hw[FU];   // the history bitmap words of this tile, read together
+        if (pen_on) {
+#pragma unroll
+            for (int j = 0; j < FU; ++j) {
+                const int e = (t * TV + j * NT + tid) * VW;
+                hw[j] = bm[e >> 5];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < FU; ++j) {
+            float xs[VW];
+            IO::unpack(b[j], xs);
+            const int e = (t * TV + j * NT + tid) * VW;
+            if (pen_on) {
+                const uint32_t bits = (hw[j] >> (e & 31)) & ((1u << VW) - 1u);
+                if (bits) {
+#pragma unroll
+                    for (int q = 0; q < VW; ++q)
+                        if ((bits >> q) & 1u) xs[q] = penalize(xs[q], pen);
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < VW; ++q) elem(j * VW + q, e + q, xs[q]);
+        }
+    };
+
+    // two tiles in flight: A holds tile t, B tile t + 1; indices past the
+    // last whole tile load that tile again (cached, never processed)
+    vec_t A[FU], Bf[FU];
+    const int last = nfull - 1;
+    if (nfull > 0) {
+        load(A, 0);
+        load(Bf, 1 < nfull ? 1 : last);
+    }
+    auto vid = [&](int t) {
+        return [=](int i) { return (t * TV + (i / VW) * NT + tid) * VW + i % VW; };
+    };
+    for (int t = 0; t < nfull; t += 2) {
+        proc(A, t);
+        if (tile_end(vid(t))) return;
+        load(A, t + 2 < nfull ? t + 2 : last);
+        if (t + 1 < nfull) {
+            proc(Bf, t + 1);
+            if (tile_end(vid(t + 1))) return;
+        }
+        load(Bf, t + 3 < nfull ? t + 3 : last);
+    }
+    // the rest of the row (all of a row that is not 16-byte aligned), element by element
+    for (int e0 = nfull * FTILE; e0 < V; e0 += FTILE) {
+        float xs[FPT];
+#pragma unroll
+        for (int i = 0; i < FPT; ++i) {
+            const int e = e0 + i * NT + tid;
+            xs[i] = e < V ? IO::one(rowp, e) : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < FPT; ++i) {
+            const int e = e0 + i * NT + tid;
+            if (e < V) {
+                float x = xs[i];
+                if (pen_on && ((bm[e >> 5] >> (e & 31)) & 1u)) x = penalize(x, pen);
+                elem(i, e, x);
+            }
+        }
+        if (tile_end([=](int i) { return e0 + i * NT + tid; })) return;
+    }
+}
+
+// Exclusive prefix over the wave of c (0 <= c < 32) and the wave's total,
+// from bit-plane ballots (no cross-lane data movement).
+__device__ __forceinline__ uint32_t wave_excl_small(uint32_t c, uint32_t& total)
+{
+    uint32_t pre = 0, tot = 0;
+#pragma unroll
+    for (int b = 0; b < 5; ++b) {
+        const u64 m = __ballot((c >> b) & 1u);
+        pre += lanes_below(m) << b;
+        tot += (uint32_t)__builtin_popcountll(m) << b;
+    }
+    total = tot;
+    return pre;
+}
+
+template <typename TIn>
+__global__ __launch_bounds__(NT, 1) void k_fused(Params p)
+{
+    extern __shared__ __align__(16) unsigned char smem[];
+    uint32_t* ck = (uint32_t*)(smem + KF_CK);   // candidate selection keys
+    uint32_t* ci = (uint32_t*)(smem + KF_CI);   // candidate ids
+    uint32_t* bm = (uint32_t*)(smem + KF_BM);   // history bitmap
+    uint32_t* hist = (uint32_t*)(smem + KF_H);
+    __shared__ uint32_t s_cnt[3];               // appends per tile, rotating
+    __shared__ uint32_t s_seg[NWAVES];          // entries per buffer segment
+    __shared__ uint32_t s_ovf;                  // a segment ran full
+
+    const int tid = threadIdx.x, lane = lane_id();
+    const int r = blockIdx.x;
+    const int V = p.V;
+    const float T = p.T[r];
+    const int k = p.K[r];
+    const float pen = p.PEN[r];
+    RowMode mode = classify(T, k, V);
+    const bool neg = T < 0.0f;
+    const TIn* rowp = (const TIn*)p.logits + (size_t)r * (size_t)p.ld;
+    const int h0 = p.hoff ? p.hoff[r] : 0;
+    const int h1 = p.hoff ? p.hoff[r + 1] : 0;
+    const bool pen_on = (pen != 1.0f) && (h1 > h0);
+    const float top_p = p.P[r];
+    const float u = p.U ? p.U[r] : 0.0f;
+    int64_t tok = -1;
+    int32_t st = MXS_ROW_OK;
+
+    if (p.out_probs) {
+        float* o = p.out_probs + (size_t)r * (size_t)V;
+        for (int i = tid; i < V; i += NT) o[i] = 0.0f;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");   // before the writes of the kept probabilities
+    }
+    if (tid < 3) s_cnt[tid] = 0;
+
+    // sampling.py:38-45: the row's history ids, each once (sorted(set()))
+    bool bad = false;
+    if (pen_on) {
+        const int words = (V + 31) >> 5;
+        for (int w = tid; w < words; w += NT) bm[w] = 0;
+        __syncthreads();
+        for (int h = h0 + tid; h < h1; h += NT) {
+            const int id = p.hids[h];
+            if (id < 0 || id >= V) { bad = true; continue; }
+            atomicOr(&bm[id >> 5], 1u << (id & 31));
+        }
+    }
+    if (block_max<uint32_t>(bad ? 1u : 0u)) st = MXS_ROW_BAD_HISTORY;   // (its barriers publish bm)
+    else if (mode == MODE_INVALID) st = MXS_ROW_BAD_PARAM;
+
+    if (st == MXS_ROW_OK && mode == MODE_GREEDY) {   // sampling.py:47-48
+        uint32_t bk = 0, bi = 0;
+        stream_row<TIn>(rowp, V, bm, pen_on, pen,
+            [&](int, int e, float x) {
+                const uint32_t g = (x != x) ? 0xFFFFFFFFu : vkey(x);   // NaN is the maximum
+                if (g > bk) { bk = g; bi = (uint32_t)e; }              // ascending e: the first maximum
+            },
+            [&](auto&&) { return false; });
+        const u64 best = block_max<u64>(bk ? (((u64)bk << 32) | (u64)(0xFFFFFFFFu - bi)) : 0ull);
+        tok = (int64_t)(0xFFFFFFFFu - (uint32_t)best);
+        if (p.out_probs && tid == 0) p.out_probs[(size_t)r * (size_t)V + (size_t)tok] = 1.0f;
+    } else if (st == MXS_ROW_OK) {
+        // selection keys of the penalized row: extremes (NaN and infinity
+        // tests, the row maximum) and, for top-k rows, the candidates
+        uint32_t omax = 0, omin = 0xFFFFFFFFu;
+        uint32_t theta = 0, Nc = 0;
+        int cidx = 0;
+        bool overflow = false;
+        const uint32_t kk = (uint32_t)k;
+        // With 1 <= pen < inf and T > 0 the penalty never raises a selection
+        // key, so the stream may compare raw keys: the raw hits include every
+        // penalized hit.  Buffered history ids get their penalized keys
+        // (fix_up) before any bound is taken from the buffer.
+        const bool defer = pen_on && !neg && pen >= 1.0f && pen <= 3.402823466e38f;
+        uint32_t Nfix = 0;   // buffer entries [0, Nfix) hold penalized keys
+        auto fix_up = [&]() {
+            if (defer) {
+                for (uint32_t j = Nfix + tid; j < Nc; j += NT) {
+                    const uint32_t id = ci[j];
+                    if ((bm[id >> 5] >> (id & 31)) & 1u) ck[j] = okey(penalize(okey_inv(ck[j]), pen));
+                }
+                __syncthreads();
+            }
+            Nfix = Nc;
+        };
+        if (mode == MODE_TOPK) {
+            // 1. A conservative estimate of the k-th largest key from a strided
+            //    sample of NSAMP logits: the lower edge of the histogram bin
+            //    holding the sample's j-th largest, j well above the expected
+            //    k * NSAMP / V.  It only steers the stream; step 3 checks it.
+            bool fast = V >= FAST_MIN_V;
+            uint32_t est = 0;
+            if (tid == 0) s_ovf = 0u;
+            if (fast) {
+                constexpr int NS = NSAMP / NT;
+                const int stride = V / NT;
+                uint32_t sk4[NS], smax = 0, smin = 0xFFFFFFFFu;
+#pragma unroll
+                for (int q = 0; q < NS; ++q) {
+                    const int e = tid * stride + q;
+                    float x = VecIO<TIn>::one(rowp, e);
+                    if (pen_on && !defer && ((bm[e >> 5] >> (e & 31)) & 1u)) x = penalize(x, pen);
+                    sk4[q] = selkey(x, neg);
+                    smax = sk4[q] > smax ? sk4[q] : smax;
+                    smin = sk4[q] < smin ? sk4[q] : smin;
+                }
+                const float ks = (float)kk * (float)NSAMP / (float)V;
+                uint32_t js = (uint32_t)ceilf(ks + 6.0f * sqrtf(ks) + 3.0f);
+                js = js < (uint32_t)NSAMP ? js : (uint32_t)NSAMP;
+                const Reduced sr = block_reduce(smax, smin, 0u);
+                const uint32_t span = sr.max - sr.min;
+                const int sh = span >= 2048u ? (32 - __builtin_clz(span)) - 11 : 0;
+                for (int b = tid; b < 2048; b += NT) hist[b] = 0;
+                __syncthreads();
+#pragma unroll
+                for (int q = 0; q < NS; ++q) atomicAdd(&hist[(sk4[q] - sr.min) >> sh], 1u);
+                __syncthreads();
+                const BinHit hb = find_desc<uint32_t>(hist, 2048, (u64)(js - 1u));
+                est = sr.min + ((uint32_t)hb.bin << sh);
+                if (est < SK_MIN) est = SK_MIN;
+                theta = widen_threshold(est, T, neg);
+            }
+            if (fast) {
+                // 2. The stream: each wave appends its hits to its own segment
+                //    of the buffer, so no barrier is needed.  A full segment
+                //    stops every wave (step 4 takes over).
+                const int w = wave_id();
+                uint32_t* wck = ck + w * FSEG;
+                uint32_t* wci = ci + w * FSEG;
+                uint32_t cw = 0;
+                uint32_t tk[FPT];   // this tile's keys
+                u64 wm[FPT];        // wave ballots of the hits, per slot
+#pragma unroll
+                for (int i = 0; i < FPT; ++i) wm[i] = 0;
+                stream_row<TIn>(rowp, V, bm, pen_on && !defer, pen,
+                    [&](int i, int, float x) {
+                        const uint32_t sk = selkey(x, neg);
+                        omax = sk > omax ? sk : omax;
+                        omin = sk < omin ? sk : omin;
+                        tk[i] = sk;
+                        wm[i] = __ballot(sk >= theta);
+                    },
+                    [&](auto&& id) -> bool {
+                        uint32_t tot = 0;
+#pragma unroll
+                        for (int i = 0; i < FPT; ++i) tot += (uint32_t)__builtin_popcountll(wm[i]);
+                        if (cw + tot > (uint32_t)FSEG) {
+                            if (lane == 0) __hip_atomic_store(&s_ovf, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                            return true;
+                        }
+#pragma unroll
+                        for (int i = 0; i < FPT; ++i) {
+                            const u64 m = wm[i];
+                            if (m) {
+                                if ((m >> lane) & 1ull) {
+                                    const uint32_t o = cw + lanes_below(m);
+                                    wck[o] = tk[i];
+                                    wci[o] = (uint32_t)id(i);
+                                }
+                                cw += (uint32_t)__builtin_popcountll(m);
+                            }
+                            wm[i] = 0;
+                        }
+                        return __hip_atomic_load(&s_ovf, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0u;
+                    });
+                if (lane == 0) s_seg[w] = cw;
+                __syncthreads();
+                fast = s_ovf == 0u;
+                if (fast) {
+                    // 3. Penalize the buffered history ids; the estimate stands
+                    //    if at least k buffered keys reach it (then the k-th
+                    //    largest key is >= est, and every element that ties
+                    //    with it after x / T is >= widen(est) = theta).
+                    uint32_t reach = 0;
+                    for (int v = 0; v < NWAVES; ++v) {
+                        const uint32_t c = s_seg[v];
+                        for (uint32_t j = tid; j < c; j += NT) {
+                            const uint32_t slot = (uint32_t)v * FSEG + j;
+                            uint32_t key = ck[slot];
+                            if (defer) {
+                                const uint32_t id = ci[slot];
+                                if ((bm[id >> 5] >> (id & 31)) & 1u) ck[slot] = key = okey(penalize(okey_inv(key), pen));
+                            }
+                            reach += key >= est ? 1u : 0u;
+                        }
+                    }
+                    fast = block_sum<uint32_t>(reach) >= kk;
+                }
+            }
+            if (!fast) {
+                // 4. The stream again with one shared buffer and a running
+                //    bound raised by compaction whenever it nears capacity.
+                theta = 0;
+                Nc = 0;
+                Nfix = 0;
+                cidx = 0;
+                if (tid < 3) s_cnt[tid] = 0;
+                __syncthreads();
+                uint32_t tk[FPT], te[FPT], hm = 0;   // this tile's keys, ids and hits
+                stream_row<TIn>(rowp, V, bm, pen_on && !defer, pen,
+                    [&](int i, int e, float x) {
+                        const uint32_t sk = selkey(x, neg);
+                        omax = sk > omax ? sk : omax;
+                        omin = sk < omin ? sk : omin;
+                        tk[i] = sk;
+                        te[i] = (uint32_t)e;
+                        hm |= (sk >= theta ? 1u : 0u) << i;
+                    },
+                    [&](auto&&) -> bool {
+                        // append this tile's hits: one LDS atomic per wave
+                        uint32_t wtot;
+                        const uint32_t pre = wave_excl_small((uint32_t)__builtin_popcount(hm), wtot);
+                        if (wtot) {
+                            uint32_t base = 0;
+                            if (lane == 0) base = atomicAdd(&s_cnt[cidx], wtot);
+                            uint32_t o = Nc + (uint32_t)__builtin_amdgcn_readfirstlane((int)base) + pre;
+#pragma unroll
+                            for (int i = 0; i < FPT; ++i) {
+                                const bool h = (hm >> i) & 1u;
+                                if (__ballot(h)) {
+                                    if (h) { ck[o] = tk[i]; ci[o] = te[i]; ++o; }
+                                }
+                            }
+                        }
+                        hm = 0;
+                        __syncthreads();
+                        Nc += s_cnt[cidx];
+                        cidx = cidx == 2 ? 0 : cidx + 1;
+                        // the counter of the tile after next: every wave has read it
+                        if (tid == 0) s_cnt[cidx == 2 ? 0 : cidx + 1] = 0;
+                        if (Nc <= (uint32_t)(FCAP - FTILE)) return false;
+                        // raise theta from the buffer, then compact it
+                        fix_up();
+                        uint32_t mx = 0, mn = 0xFFFFFFFFu;
+                        for (uint32_t j = tid; j < Nc; j += NT) {
+                            const uint32_t key = ck[j];
+                            mx = key > mx ? key : mx;
+                            mn = key < mn ? key : mn;
+                        }
+                        const Reduced rd = block_reduce(mx, mn, 0u);
+                        const uint32_t lo = rd.min, span = rd.max - rd.min;
+                        const int sh = span >= 2048u ? (32 - __builtin_clz(span)) - 11 : 0;
+                        for (int b = tid; b < 2048; b += NT) hist[b] = 0;
+                        __syncthreads();
+                        for (uint32_t j = tid; j < Nc; j += NT) atomicAdd(&hist[(ck[j] - lo) >> sh], 1u);
+                        __syncthreads();
+                        const BinHit hb = find_desc<uint32_t>(hist, 2048, (u64)(kk - 1u));
+                        uint32_t bound = lo + ((uint32_t)hb.bin << sh);
+                        if (bound < SK_MIN) bound = SK_MIN;
+                        const uint32_t nt = widen_threshold(bound, T, neg);
+                        theta = nt > theta ? nt : theta;
+                        constexpr int PER = FCAP / NT;
+                        uint32_t kv[PER], iv[PER], keep = 0;
+#pragma unroll
+                        for (int q = 0; q < PER; ++q) {
+                            const uint32_t j = (uint32_t)(tid + q * NT);
+                            kv[q] = j < Nc ? ck[j] : 0u;
+                            iv[q] = j < Nc ? ci[j] : 0u;
+                            keep += (j < Nc && kv[q] >= theta) ? 1u : 0u;
+                        }
+                        uint32_t total;
+                        uint32_t o = block_incl_scan<uint32_t>(keep, &total) - keep;   // its barriers end the reads
+#pragma unroll
+                        for (int q = 0; q < PER; ++q) {
+                            const uint32_t j = (uint32_t)(tid + q * NT);
+                            if (j < Nc && kv[q] >= theta) { ck[o] = kv[q]; ci[o] = iv[q]; ++o; }
+                        }
+                        Nc = total;
+                        Nfix = total;
+                        __syncthreads();
+                        if (Nc > (uint32_t)(FCAP - FTILE)) { overflow = true; return true; }   // massive ties
+                        return false;
+                    });
+                if (!overflow) fix_up();
+                if (tid < NWAVES) s_seg[tid] = tid == 0 ? Nc : 0u;
+                __syncthreads();
+            }
+        } else {
+            stream_row<TIn>(rowp, V, bm, pen_on, pen,
+                [&](int, int, float x) {
+                    const uint32_t sk = selkey(x, neg);
+                    omax = sk > omax ? sk : omax;
+                    omin = sk < omin ? sk : omin;
+                },
+                [&](auto&&) { return false; });
+        }
+        const Reduced rd = block_reduce(omax, omin, 0u);
+        // NaN keys lie above the key of +inf and below that of -inf (the
+        // reversed keys of T < 0 swap the two ranges)
+        const bool has_nan = rd.max > 0xFF800000u || rd.min < 0x007FFFFFu;
+        const bool has_inf = rd.max >= 0xFF800000u || rd.min <= 0x007FFFFFu;
+        if (has_nan || (has_inf && __builtin_isinf(T))) {
+            st = MXS_ROW_NONFINITE;   // a NaN tempered logit heads the order (sampling.py:57-58)
+        } else {
+            bool done = false;
+            uint32_t thk = 0;
+            bool thk_known = false;
+            if (mode == MODE_TOPK && !overflow) {
+                auto for_slots = [&](auto&& f) {
+                    for (int v = 0; v < NWAVES; ++v) {
+                        const uint32_t c = s_seg[v];
+                        for (uint32_t j = tid; j < c; j += NT) f((uint32_t)v * FSEG + j);
+                    }
+                };
+                auto visit = [&](auto&& f) { for_slots([&](uint32_t slot) { f(ck[slot]); }); };
+                // sampling.py:52-54: the k-th largest, then everything that rounds onto it
+                uint32_t sk_k = select_exact(kk, visit, hist);
+                if (sk_k < SK_MIN) sk_k = SK_MIN;
+                thk = widen_threshold(sk_k, T, neg);
+                thk_known = true;
+                uint32_t mine = 0;
+                visit([&](uint32_t sk) { mine += sk >= thk ? 1u : 0u; });
+                uint32_t n1u;
+                uint32_t o = block_incl_scan<uint32_t>(mine, &n1u) - mine;
+                if (n1u <= (uint32_t)SORT_CAP) {
+                    u64* keys = (u64*)(smem + KF_BM);
+                    for_slots([&](uint32_t slot) {
+                        const uint32_t sk = ck[slot];
+                        if (sk >= thk) {
+                            const uint32_t vk = vkey(sel_inv(sk, neg) / T);
+                            keys[o++] = ((u64)vk << 32) | (u64)(0xFFFFFFFFu - ci[slot]);
+                        }
+                    });
+                    __syncthreads();
+                    done = finish_kept(p, r, keys, (u64*)(smem + KF_CK), (int)n1u, top_p, u,
+                                       (u64*)(smem + KF_MH), hist, tok, st);
+                }
+            }
+            if (!done) {
+                __syncthreads();
+                const LargeLds lds{bm, (u64*)(smem + KF_MH), (u64*)(smem + KF_CK), hist};
+                const uint32_t skmax = rd.max;
+                const bool raw_max = defer && mode == MODE_TOPK;   // then the maximum is taken again
+                finish_large<TIn>(p, r, T, k, top_p, pen, pen_on, true, skmax, !raw_max, thk_known, thk, u, lds,
+                                  tok, st);
+            }
         }
     }
     if (tid == 0) {
@@ -1145,9 +1633,22 @@ Layout layout(int B, int V)
     return L;
 }
 
+// Batches of at least this many rows run one workgroup per row (k_fused);
+// smaller ones split rows into chunks across more workgroups.
+#ifndef MXS_FUSED_MIN_B
+#define MXS_FUSED_MIN_B 128
+#endif
+
 template <typename TIn>
 hipError_t launch(const Params& p, hipStream_t s)
 {
+    if (p.B >= MXS_FUSED_MIN_B) {
+        static const hipError_t a0 = hipFuncSetAttribute((const void*)k_fused<TIn>,
+                                                         hipFuncAttributeMaxDynamicSharedMemorySize, KF_LDS_BYTES);
+        (void)a0;
+        hipLaunchKernelGGL(k_fused<TIn>, dim3((unsigned)p.B), dim3(NT), KF_LDS_BYTES, s, p);
+        return hipGetLastError();
+    }
     static const hipError_t a1 = hipFuncSetAttribute((const void*)k_chunks<TIn>,
                                                      hipFuncAttributeMaxDynamicSharedMemorySize, K1_LDS_BYTES);
     static const hipError_t a2 = hipFuncSetAttribute((const void*)k_rows<TIn>,

@@ -59,7 +59,7 @@ enum {
     ORC_ROW_OK = 0,
     ORC_ROW_BAD_HISTORY = 1,   /* history id outside [0, V) */
     ORC_ROW_BAD_PARAM = 2,     /* temperature is NaN */
-    ORC_ROW_NONFINITE = 3,     /* max tempered logit is inf or NaN */
+    ORC_ROW_NONFINITE = 3,     /* a tempered logit is NaN, or the maximum is infinite */
     ORC_ROW_EMPTY_NUCLEUS = 4  /* top_p <= 0 removes every token */
 };
 
@@ -229,7 +229,12 @@ static int sample_row(const float* xin, int V, float T, int k, float p, float pe
 
     /* sampling.py:50 */
     float* l = s->l;
-    for (int i = 0; i < V; ++i) l[i] = x[i] / T;
+    /* a NaN anywhere (a NaN logit, or an infinite one over an infinite T)
+     * makes torch's softmax NaN throughout and multinomial reject the row,
+     * whatever the NaN's sign bit (sampling.py:58, 68-69) */
+    int any_nan = 0;
+    for (int i = 0; i < V; ++i) { l[i] = x[i] / T; any_nan |= isnan(l[i]); }
+    if (any_nan) { inf.status = ORC_ROW_NONFINITE; goto done; }
 
     /* sort by (value desc, index asc): ascending (~vkey, index) */
     uint64_t* ord = s->ord;

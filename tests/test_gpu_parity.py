@@ -102,6 +102,11 @@ def _edge_rows(V, seed=7):
     rows.append((0.05, 40, 0.9, 1.0, [], 0.0))                # u = 0
     rows.append((1.0, 1024, 0.99, 1.0, [], 0.61))             # k = KMAX
     rows.append((1.0, 1025, 0.99, 1.0, [], 0.61))             # k just above KMAX
+    top = [int(i) for i in np.argsort(-base, kind="stable")[:100]]
+    rows.append((0.9, 50, 0.9, 5.0, top, 0.42))                # heavy penalty on the row's top ids
+    rows.append((0.9, 30, 0.9, 0.8, top[:40] + [1, 2], 0.77))  # penalty < 1 on a top-k row
+    rows.append((-0.7, 25, 0.95, 1.3, top + [3, 4], 0.33))     # negative temperature with a penalty
+    rows.append((1.1, 1000, 0.97, 1.15, list(range(0, V, 3)), 0.5))   # a third of the row penalized
     return base, rows
 
 
@@ -128,6 +133,10 @@ def test_parity_ties_and_infinities(oracle, cuda):
     q = np.round(np.random.default_rng(3).standard_normal(V) * 4).astype(np.float32)
     rows.append(q); params.append((0.9, 300, 0.9, 1.1, [1, 2, 3], 0.55))                   # coarse ties
     rows.append(q.copy()); params.append((float("inf"), 0, 0.3, 1.0, [], 0.5))             # T = inf
+    qi = q.copy(); qi[1234] = -np.inf
+    rows.append(qi); params.append((float("inf"), 20, 0.9, 1.0, [], 0.5))                  # inf / inf
+    qn = q.copy(); qn[777] = np.frombuffer(np.uint32(0xFFC00000).tobytes(), np.float32)[0]
+    rows.append(qn); params.append((0.8, 20, 0.9, 1.0, [], 0.5))                           # negative NaN
     T, k, p, pen, h, u = (list(c) for c in zip(*params))
     w = custom("ties", np.stack(rows), T, k, p, pen, h, u)
     say(f"[ties] rows={w.B}")
@@ -180,3 +189,52 @@ def test_workspace_reuse_across_batch_sizes(oracle, cuda):
         ref = run_oracle(oracle, w, probs=False)
         tok, st, _ = run_gpu(w, cuda, probs=False)
         check(w, ref, tok, st, None)
+
+
+def test_parity_one_workgroup_per_row_fallbacks(oracle, cuda):
+    """A batch large enough for one workgroup per row, with rows built to
+    defeat the sampled first bound: sampled positions that overstate the top
+    values (the estimate fails its check and the row is streamed again with a
+    compacted buffer), top values hidden between the sampled positions, a
+    20000-way tie that overflows every buffer (multi-pass path), and rows
+    that apply the penalty while streaming (T < 0, penalty < 1, greedy)."""
+    V = VOCAB
+    stride = V // 512
+    rng = np.random.default_rng(11)
+    rows, params = [], []
+    r = (2.0 * rng.standard_normal(V)).astype(np.float32)
+    r[np.arange(512) * stride] = 50.0
+    rows.append(r); params.append((1.0, 700, 0.9, 1.0, [], 0.3))         # estimate too high
+    r = (2.0 * rng.standard_normal(V)).astype(np.float32)
+    r[np.arange(512) * stride + 8] = 30.0 + rng.random(512).astype(np.float32)
+    rows.append(r); params.append((0.8, 300, 0.95, 1.1, list(range(0, V, 97)), 0.6))   # hidden top values
+    r = (2.0 * rng.standard_normal(V)).astype(np.float32)
+    r[rng.choice(V, 20000, replace=False)] = 5.0
+    rows.append(r); params.append((1.0, 100, 0.9, 1.0, [], 0.45))        # ties overflow the buffer
+    r = (2.0 * rng.standard_normal(V)).astype(np.float32)
+    rows.append(r); params.append((-0.6, 40, 0.9, 1.4, list(range(5, V, 11)), 0.8))   # T < 0, penalty
+    r = (2.0 * rng.standard_normal(V)).astype(np.float32)
+    rows.append(r); params.append((0.7, 60, 0.85, 0.6, list(range(7, V, 13)), 0.1))   # penalty < 1
+    r = (2.0 * rng.standard_normal(V)).astype(np.float32)
+    top = [int(i) for i in np.argsort(-r)[:3]]
+    rows.append(r); params.append((0.0, 0, 1.0, 3.0, top, 0.0))           # greedy with a penalty
+    r = (2.0 * rng.standard_normal(V)).astype(np.float32)
+    r[99] = np.inf
+    rows.append(r); params.append((float("inf"), 50, 0.9, 1.0, [], 0.5))  # inf / inf: non-finite
+    r = (2.0 * rng.standard_normal(V)).astype(np.float32)
+    r[4242] = np.frombuffer(np.uint32(0xFFC00000).tobytes(), np.float32)[0]
+    rows.append(r); params.append((0.9, 50, 0.9, 1.2, [4242, 7], 0.5))   # a negative NaN
+    z = make_workload("zipf", B=128 - len(rows))
+    x = np.concatenate([np.stack(rows), z.logits])
+    T = [p[0] for p in params] + z.temperature.tolist()
+    k = [p[1] for p in params] + z.top_k.tolist()
+    pp = [p[2] for p in params] + z.top_p.tolist()
+    pen = [p[3] for p in params] + z.penalty.tolist()
+    hists = [p[4] for p in params] + [z.hist_ids[z.hist_offsets[i]:z.hist_offsets[i + 1]].tolist()
+                                      for i in range(z.B)]
+    u = [p[5] for p in params] + z.uniforms.tolist()
+    w = custom("fused-fallbacks", x, T, k, pp, pen, hists, u)
+    say(f"[fused-fallbacks] rows={w.B}")
+    ref = run_oracle(oracle, w, probs=False)
+    tok, st, _ = run_gpu(w, cuda, probs=False)
+    check(w, ref, tok, st, None)

@@ -315,5 +315,11 @@ def test_row_statuses(oracle):
     y = x.copy(); y[3] = np.inf
     assert run(oracle, y, 0.8)[:2] == (-1, 3)                            # inf after temperature
     assert run(oracle, y, 0.0)[:2] == (3, 0)                             # greedy takes the inf
+    assert run(oracle, y, float("inf"))[:2] == (-1, 3)                   # inf / inf is NaN
+    z = x.copy(); z[5] = -1.0
+    assert run(oracle, z, float("inf"))[1] == 0                          # finite / inf is 0
+    n = x.copy(); n[9] = np.frombuffer(np.uint32(0xFFC00000).tobytes(), np.float32)[0]
+    assert run(oracle, n, 0.8)[:2] == (-1, 3)                            # a NaN of either sign
+    assert run(oracle, n, 0.8, k=2)[:2] == (-1, 3)
     assert run(oracle, x, 0.8, p=0.0)[:2] == (-1, 4)                     # top_p <= 0 keeps nothing
     assert run(oracle, x, 0.8, p=-1.0)[:2] == (-1, 4)
