@@ -781,36 +781,64 @@ __device__ __forceinline__ uint32_t rank_in_range(Visit visit, uint32_t blo, uin
     return res;
 }
 
-// Exact kk-th largest (1-based) key.  Each level histograms the keys of the
-// current range into 2048 bins spanning exactly that range; a bin of at most
-// 64 keys is finished by ranking, otherwise it becomes the next range.
+// The value a selection key stands for, ordered like the key: x, or -x
+// when T < 0.
+__device__ __forceinline__ float sel_val(uint32_t s, bool neg)
+{
+    const float x = sel_inv(s, neg);
+    return neg ? -x : x;
+}
+
+// Exact kk-th largest (1-based) selection key.  Each level histograms the
+// keys of the current range into 2048 bins that are linear in the value the
+// keys stand for (key-space bins when the range is not finite); the bin
+// holding the answer is a contiguous key range because the bin function is
+// monotone.  A bin of at most 64 keys is finished by ranking, otherwise it
+// becomes the next range; lo and hi fall into different bins, so every level
+// narrows the range.
 template <class Visit>
-__device__ __forceinline__ uint32_t select_exact(uint32_t kk, Visit visit, uint32_t* hist)
+__device__ __forceinline__ uint32_t select_exact(uint32_t kk, Visit visit, uint32_t* hist, bool neg)
 {
     uint32_t mx = 0, mn = 0xFFFFFFFFu;
     visit([&](uint32_t k) { mx = k > mx ? k : mx; mn = k < mn ? k : mn; });
     const Reduced rd = block_reduce(mx, mn, 0u);
     uint32_t lo = rd.min, hi = rd.max;
-    for (int lev = 0; lev < 4 && lo != hi; ++lev) {
+    for (int lev = 0; lev < 64 && lo != hi; ++lev) {
+        const float ylo = sel_val(lo, neg), yhi = sel_val(hi, neg);
+        const float scale = 2047.0f / (yhi - ylo);
+        const bool lin = __builtin_isfinite(ylo) && __builtin_isfinite(yhi) && yhi > ylo && scale > 0.0f &&
+                         __builtin_isfinite(scale);
         const uint32_t span = hi - lo;
         const int sh = span >= 2048u ? (32 - __builtin_clz(span)) - 11 : 0;
+        auto bin_of = [&](uint32_t k) -> uint32_t {
+            if (lin) {
+                const float f = (sel_val(k, neg) - ylo) * scale;
+                return f < 2047.0f ? (uint32_t)f : 2047u;
+            }
+            return (k - lo) >> sh;
+        };
         for (int b = threadIdx.x; b < 2048; b += NT) hist[b] = 0;
         __syncthreads();
         visit([&](uint32_t k) {
-            if (k >= lo && k <= hi) atomicAdd(&hist[(k - lo) >> sh], 1u);
+            if (k >= lo && k <= hi) atomicAdd(&hist[bin_of(k)], 1u);
         });
         __syncthreads();
         const BinHit hit = find_desc<uint32_t>(hist, 2048, (u64)(kk - 1u));
         const uint32_t cnt = hist[hit.bin];
-        const uint32_t blo = lo + ((uint32_t)hit.bin << sh);
-        const u64 top = (u64)blo + ((u64)1 << sh) - 1;
-        const uint32_t bhi = top < (u64)hi ? (uint32_t)top : hi;
         kk -= (uint32_t)hit.above;
         __syncthreads();
-        if (sh == 0) return blo;
-        if (cnt <= 64u) return rank_in_range(visit, blo, bhi, cnt, kk - 1u);
-        lo = blo;
-        hi = bhi;
+        if (!lin && sh == 0) return lo + (uint32_t)hit.bin;
+        uint32_t bmx = 0, bmn = 0xFFFFFFFFu;
+        visit([&](uint32_t k) {
+            if (k >= lo && k <= hi && bin_of(k) == (uint32_t)hit.bin) {
+                bmx = k > bmx ? k : bmx;
+                bmn = k < bmn ? k : bmn;
+            }
+        });
+        const Reduced br = block_reduce(bmx, bmn, 0u);
+        if (cnt <= 64u) return rank_in_range(visit, br.min, br.max, cnt, kk - 1u);
+        lo = br.min;
+        hi = br.max;
     }
     return lo;
 }
@@ -907,8 +935,26 @@ __device__ __forceinline__ bool finish_kept(const Params& p, int r, u64* keys, u
     const Reduced rd = block_reduce(vmax, vmin, 0u);
     const float m = okey_inv(rd.max);
     if (!isfinite(m)) { st = MXS_ROW_NONFINITE; tok = -1; return true; }
-    const uint32_t span = rd.max - rd.min;
-    const int sh = span >= 2048u ? (32 - __builtin_clz(span)) - 11 : 0;
+    // Bins linear in d = l - m over [dmin, 0] (d = -inf in bin 0): monotone
+    // in the sorted order, and spread evenly where float keys are not.
+    float dmin = okey_inv(rd.min) - m;
+    if (!(dmin > -INFINITY)) {   // -inf logits are kept: the smallest finite d
+        uint32_t fmn = 0xFFFFFFFFu;
+        for (int j = threadIdx.x; j < n; j += NT) {
+            const uint32_t vk = (uint32_t)(keys[j] >> 32);
+            if (vk > SK_MIN) fmn = vk < fmn ? vk : fmn;
+        }
+        const uint32_t f = block_reduce(0u, fmn, 0u).min;
+        dmin = f == 0xFFFFFFFFu ? 0.0f : okey_inv(f) - m;
+    }
+    float scale = dmin < 0.0f ? 2047.0f / -dmin : 0.0f;
+    if (!__builtin_isfinite(scale)) scale = 0.0f;
+    auto bin_of = [&](uint32_t vk) -> uint32_t {
+        const float d = okey_inv(vk) - m;
+        if (!(d > -INFINITY)) return 0u;
+        const float f = (d - dmin) * scale;
+        return f < 2047.0f ? (uint32_t)f : 2047u;
+    };
     for (int b = threadIdx.x; b < 2048; b += NT) { MH[b] = 0; CH[b] = 0; }
     __syncthreads();
     u64 part = 0;
@@ -917,7 +963,7 @@ __device__ __forceinline__ bool finish_kept(const Params& p, int r, u64* keys, u
         const u64 w = mass_of(okey_inv(vk) - m);
         wm[j] = w;
         part += w;
-        const uint32_t bin = (vk - rd.min) >> sh;
+        const uint32_t bin = bin_of(vk);
         atomicAdd(&MH[bin], w);
         atomicAdd(&CH[bin], 1u);
     }
@@ -931,7 +977,7 @@ __device__ __forceinline__ bool finish_kept(const Params& p, int r, u64* keys, u
         __syncthreads();
         if (cnt <= 64u) {
             for (int j = threadIdx.x; j < n; j += NT) {
-                if ((((uint32_t)(keys[j] >> 32) - rd.min) >> sh) == (uint32_t)hit.bin) {
+                if (bin_of((uint32_t)(keys[j] >> 32)) == (uint32_t)hit.bin) {
                     const uint32_t slot = atomicAdd(&g_n, 1u);
                     if (slot < 64u) { g_key[slot] = keys[j]; g_w[slot] = wm[j]; }
                 }
@@ -1039,7 +1085,7 @@ __device__ __forceinline__ bool finish_topk(const Params& p, int r, float T, int
     };
 
     // sampling.py:52-54: the k-th largest, then everything that rounds onto it
-    uint32_t sk_k = select_exact(kk, visit, hist);
+    uint32_t sk_k = select_exact(kk, visit, hist, neg);
     if (sk_k < SK_MIN) sk_k = SK_MIN;
     const uint32_t theta = widen_threshold(sk_k, T, neg);
     uint32_t mine = 0;
@@ -1577,7 +1623,7 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                 };
                 auto visit = [&](auto&& f) { for_slots([&](uint32_t slot) { f(ck[slot]); }); };
                 // sampling.py:52-54: the k-th largest, then everything that rounds onto it
-                uint32_t sk_k = select_exact(kk, visit, hist);
+                uint32_t sk_k = select_exact(kk, visit, hist, neg);
                 if (sk_k < SK_MIN) sk_k = SK_MIN;
                 thk = widen_threshold(sk_k, T, neg);
                 thk_known = true;
