@@ -789,6 +789,40 @@ __device__ __forceinline__ float sel_val(uint32_t s, bool neg)
     return neg ? -x : x;
 }
 
+// The r-th largest (0-based) of the cnt <= 64 keys for which in_bin holds.
+template <class Visit, class InBin>
+__device__ __forceinline__ uint32_t rank_in_bin(Visit visit, InBin in_bin, uint32_t cnt, uint32_t r)
+{
+    __shared__ uint32_t g_keys[64];
+    __shared__ uint32_t g_n, g_res;
+    if (threadIdx.x == 0) { g_n = 0; g_res = 0; }
+    __syncthreads();
+    visit([&](uint32_t k) {
+        if (in_bin(k)) {
+            const uint32_t slot = atomicAdd(&g_n, 1u);
+            if (slot < 64u) g_keys[slot] = k;
+        }
+    });
+    __syncthreads();
+    if (wave_id() == 0) {
+        const uint32_t lane = (uint32_t)lane_id();
+        const uint32_t n = g_n < cnt ? g_n : cnt;
+        const uint32_t mine = lane < n ? g_keys[lane] : 0u;
+        uint32_t gt = 0, ge = 0;
+        for (uint32_t t = 0; t < n; ++t) {   // broadcast reads of the gathered keys
+            const uint32_t other = g_keys[t];
+            gt += other > mine ? 1u : 0u;
+            ge += other >= mine ? 1u : 0u;
+        }
+        const u64 mask = __ballot(lane < n && gt <= r && r < ge);
+        if (mask && lane == (uint32_t)__builtin_ctzll(mask)) g_res = mine;
+    }
+    __syncthreads();
+    const uint32_t res = g_res;
+    __syncthreads();
+    return res;
+}
+
 // Exact kk-th largest (1-based) selection key.  Each level histograms the
 // keys of the current range into 2048 bins that are linear in the value the
 // keys stand for (key-space bins when the range is not finite); the bin
@@ -796,13 +830,11 @@ __device__ __forceinline__ float sel_val(uint32_t s, bool neg)
 // monotone.  A bin of at most 64 keys is finished by ranking, otherwise it
 // becomes the next range; lo and hi fall into different bins, so every level
 // narrows the range.
+// Keys outside [lo, hi] are ignored; at least kk keys must lie inside.
 template <class Visit>
-__device__ __forceinline__ uint32_t select_exact(uint32_t kk, Visit visit, uint32_t* hist, bool neg)
+__device__ __forceinline__ uint32_t select_exact_in(uint32_t kk, Visit visit, uint32_t* hist, bool neg,
+                                                    uint32_t lo, uint32_t hi)
 {
-    uint32_t mx = 0, mn = 0xFFFFFFFFu;
-    visit([&](uint32_t k) { mx = k > mx ? k : mx; mn = k < mn ? k : mn; });
-    const Reduced rd = block_reduce(mx, mn, 0u);
-    uint32_t lo = rd.min, hi = rd.max;
     for (int lev = 0; lev < 64 && lo != hi; ++lev) {
         const float ylo = sel_val(lo, neg), yhi = sel_val(hi, neg);
         const float scale = 2047.0f / (yhi - ylo);
@@ -828,6 +860,11 @@ __device__ __forceinline__ uint32_t select_exact(uint32_t kk, Visit visit, uint3
         kk -= (uint32_t)hit.above;
         __syncthreads();
         if (!lin && sh == 0) return lo + (uint32_t)hit.bin;
+        if (cnt <= 64u) {
+            const uint32_t b = (uint32_t)hit.bin;
+            return rank_in_bin(visit, [&](uint32_t k) { return k >= lo && k <= hi && bin_of(k) == b; },
+                               cnt, kk - 1u);
+        }
         uint32_t bmx = 0, bmn = 0xFFFFFFFFu;
         visit([&](uint32_t k) {
             if (k >= lo && k <= hi && bin_of(k) == (uint32_t)hit.bin) {
@@ -836,11 +873,19 @@ __device__ __forceinline__ uint32_t select_exact(uint32_t kk, Visit visit, uint3
             }
         });
         const Reduced br = block_reduce(bmx, bmn, 0u);
-        if (cnt <= 64u) return rank_in_range(visit, br.min, br.max, cnt, kk - 1u);
         lo = br.min;
         hi = br.max;
     }
     return lo;
+}
+
+template <class Visit>
+__device__ __forceinline__ uint32_t select_exact(uint32_t kk, Visit visit, uint32_t* hist, bool neg)
+{
+    uint32_t mx = 0, mn = 0xFFFFFFFFu;
+    visit([&](uint32_t k) { mx = k > mx ? k : mx; mn = k < mn ? k : mn; });
+    const Reduced rd = block_reduce(mx, mn, 0u);
+    return select_exact_in(kk, visit, hist, neg, rd.min, rd.max);
 }
 
 // Fallback of finish_kept for heavy ties: bitonic sort of the kept set, then
@@ -1486,24 +1531,34 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                 __syncthreads();
                 fast = s_ovf == 0u;
                 if (fast) {
-                    // 3. Penalize the buffered history ids; the estimate stands
-                    //    if at least k buffered keys reach it (then the k-th
-                    //    largest key is >= est, and every element that ties
-                    //    with it after x / T is >= widen(est) = theta).
-                    uint32_t reach = 0;
-                    for (int v = 0; v < NWAVES; ++v) {
-                        const uint32_t c = s_seg[v];
-                        for (uint32_t j = tid; j < c; j += NT) {
-                            const uint32_t slot = (uint32_t)v * FSEG + j;
-                            uint32_t key = ck[slot];
-                            if (defer) {
-                                const uint32_t id = ci[slot];
-                                if ((bm[id >> 5] >> (id & 31)) & 1u) ck[slot] = key = okey(penalize(okey_inv(key), pen));
-                            }
-                            reach += key >= est ? 1u : 0u;
-                        }
+                    // 3. One pass over the segments in registers: penalize the
+                    //    buffered history ids, count the keys that reach the
+                    //    estimate, and pack the segments into [0, Nc).  The
+                    //    estimate stands if at least k keys reach it (then the
+                    //    k-th largest key is >= est, and every element that
+                    //    ties with it after x / T is >= widen(est) = theta).
+                    constexpr int PER = FCAP / NT;
+                    uint32_t kv[PER], iv[PER], nv = 0, nr = 0;
+#pragma unroll
+                    for (int q = 0; q < PER; ++q) {
+                        const uint32_t slot = (uint32_t)(tid + q * NT);
+                        const bool valid = (slot % FSEG) < s_seg[slot / FSEG];
+                        kv[q] = valid ? ck[slot] : 0u;
+                        iv[q] = valid ? ci[slot] : 0xFFFFFFFFu;
+                        if (valid && defer && ((bm[iv[q] >> 5] >> (iv[q] & 31)) & 1u))
+                            kv[q] = okey(penalize(okey_inv(kv[q]), pen));
+                        nv += valid ? 1u : 0u;
+                        nr += (valid && kv[q] >= est) ? 1u : 0u;
                     }
-                    fast = block_sum<uint32_t>(reach) >= kk;
+                    uint32_t tot;
+                    uint32_t o = block_incl_scan<uint32_t>(nv | (nr << 16), &tot) - (nv | (nr << 16));
+                    o &= 0xFFFFu;   // (its barriers end the reads)
+#pragma unroll
+                    for (int q = 0; q < PER; ++q)
+                        if (iv[q] != 0xFFFFFFFFu) { ck[o] = kv[q]; ci[o] = iv[q]; ++o; }
+                    Nc = tot & 0xFFFFu;
+                    fast = (tot >> 16) >= kk;
+                    __syncthreads();
                 }
             }
             if (!fast) {
@@ -1591,8 +1646,6 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                         return false;
                     });
                 if (!overflow) fix_up();
-                if (tid < NWAVES) s_seg[tid] = tid == 0 ? Nc : 0u;
-                __syncthreads();
             }
         } else {
             stream_row<TIn>(rowp, V, bm, pen_on, pen,
@@ -1615,15 +1668,13 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
             uint32_t thk = 0;
             bool thk_known = false;
             if (mode == MODE_TOPK && !overflow) {
-                auto for_slots = [&](auto&& f) {
-                    for (int v = 0; v < NWAVES; ++v) {
-                        const uint32_t c = s_seg[v];
-                        for (uint32_t j = tid; j < c; j += NT) f((uint32_t)v * FSEG + j);
-                    }
+                auto visit = [&](auto&& f) {
+                    for (uint32_t j = tid; j < Nc; j += NT) f(ck[j]);
                 };
-                auto visit = [&](auto&& f) { for_slots([&](uint32_t slot) { f(ck[slot]); }); };
-                // sampling.py:52-54: the k-th largest, then everything that rounds onto it
-                uint32_t sk_k = select_exact(kk, visit, hist, neg);
+                // sampling.py:52-54: the k-th largest, then everything that rounds onto it.
+                // At least k buffered keys lie in [theta, row maximum] (keys that
+                // the penalty took below theta are not among the top k).
+                uint32_t sk_k = select_exact_in(kk, visit, hist, neg, theta, rd.max);
                 if (sk_k < SK_MIN) sk_k = SK_MIN;
                 thk = widen_threshold(sk_k, T, neg);
                 thk_known = true;
@@ -1633,13 +1684,13 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                 uint32_t o = block_incl_scan<uint32_t>(mine, &n1u) - mine;
                 if (n1u <= (uint32_t)SORT_CAP) {
                     u64* keys = (u64*)(smem + KF_BM);
-                    for_slots([&](uint32_t slot) {
-                        const uint32_t sk = ck[slot];
+                    for (uint32_t j = tid; j < Nc; j += NT) {
+                        const uint32_t sk = ck[j];
                         if (sk >= thk) {
                             const uint32_t vk = vkey(sel_inv(sk, neg) / T);
-                            keys[o++] = ((u64)vk << 32) | (u64)(0xFFFFFFFFu - ci[slot]);
+                            keys[o++] = ((u64)vk << 32) | (u64)(0xFFFFFFFFu - ci[j]);
                         }
-                    });
+                    }
                     __syncthreads();
                     done = finish_kept(p, r, keys, (u64*)(smem + KF_CK), (int)n1u, top_p, u,
                                        (u64*)(smem + KF_MH), hist, tok, st);
