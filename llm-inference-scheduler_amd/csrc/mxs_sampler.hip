@@ -1259,8 +1259,12 @@ __global__ __launch_bounds__(NT, 1) void k_rows(Params p)
 // processed (conditional loads would make the compiler wait for all of them).
 constexpr int FPT = FTILE / NT;   // logits per thread per tile (16)
 
-template <typename TIn, class Elem, class TileEnd>
-__device__ __forceinline__ void stream_row(const TIn* rowp, int V, const uint32_t* bm, bool pen_on, float pen,
+// PEN: apply the penalty from the bitmap while streaming (a separate
+// instantiation, so that rows without it carry no branches in the loop: a
+// branch around loads or their uses makes the compiler wait for every load
+// in flight).
+template <typename TIn, bool PEN, class Elem, class TileEnd>
+__device__ __forceinline__ void stream_row(const TIn* rowp, int V, const uint32_t* bm, float pen,
                                            Elem&& elem, TileEnd&& tile_end)
 {
     typedef VecIO<TIn> IO;
@@ -1279,7 +1283,7 @@ __device__ __forceinline__ void stream_row(const TIn* rowp, int V, const uint32_
     };
     auto proc = [&](const vec_t (&b)[FU], int t) {
         uint32_t hw[FU];   // the history bitmap words of this tile, read together
-        if (pen_on) {
+        if constexpr (PEN) {
 #pragma unroll
             for (int j = 0; j < FU; ++j) {
                 const int e = (t * TV + j * NT + tid) * VW;
@@ -1291,7 +1295,7 @@ __device__ __forceinline__ void stream_row(const TIn* rowp, int V, const uint32_
             float xs[VW];
             IO::unpack(b[j], xs);
             const int e = (t * TV + j * NT + tid) * VW;
-            if (pen_on) {
+            if constexpr (PEN) {
                 const uint32_t bits = (hw[j] >> (e & 31)) & ((1u << VW) - 1u);
                 if (bits) {
 #pragma unroll
@@ -1338,12 +1342,23 @@ __device__ __forceinline__ void stream_row(const TIn* rowp, int V, const uint32_
             const int e = e0 + i * NT + tid;
             if (e < V) {
                 float x = xs[i];
-                if (pen_on && ((bm[e >> 5] >> (e & 31)) & 1u)) x = penalize(x, pen);
+                if constexpr (PEN) {
+                    if ((bm[e >> 5] >> (e & 31)) & 1u) x = penalize(x, pen);
+                }
                 elem(i, e, x);
             }
         }
         if (tile_end([=](int i) { return e0 + i * NT + tid; })) return;
     }
+}
+
+// stream_row with the inline penalty chosen at run time.
+template <typename TIn, class Elem, class TileEnd>
+__device__ __forceinline__ void stream_row_pen(const TIn* rowp, int V, const uint32_t* bm, bool pen_inline, float pen,
+                                               Elem&& elem, TileEnd&& tile_end)
+{
+    if (pen_inline) stream_row<TIn, true>(rowp, V, bm, pen, elem, tile_end);
+    else stream_row<TIn, false>(rowp, V, bm, pen, elem, tile_end);
 }
 
 // Exclusive prefix over the wave of c (0 <= c < 32) and the wave's total,
@@ -1372,6 +1387,7 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
     __shared__ uint32_t s_cnt[3];               // appends per tile, rotating
     __shared__ uint32_t s_seg[NWAVES];          // entries per buffer segment
     __shared__ uint32_t s_ovf;                  // a segment ran full
+    __shared__ uint32_t s_reach[NWAVES];        // keys reaching the estimate, per segment
 
     const int tid = threadIdx.x, lane = lane_id();
     const int r = blockIdx.x;
@@ -1390,6 +1406,17 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
     int64_t tok = -1;
     int32_t st = MXS_ROW_OK;
 
+    // top-k rows: the strided sample for the first bound is requested first,
+    // so that its latency overlaps the set-up below
+    const bool sampled = mode == MODE_TOPK && V >= FAST_MIN_V;
+    constexpr int NS = NSAMP / NT;
+    float sx[NS];
+    if (sampled) {
+        const int stride = V / NT;
+#pragma unroll
+        for (int q = 0; q < NS; ++q) sx[q] = VecIO<TIn>::one(rowp, tid * stride + q);
+        for (int b = tid; b < 2048; b += NT) hist[b] = 0;
+    }
     if (p.out_probs) {
         float* o = p.out_probs + (size_t)r * (size_t)V;
         for (int i = tid; i < V; i += NT) o[i] = 0.0f;
@@ -1414,7 +1441,7 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
 
     if (st == MXS_ROW_OK && mode == MODE_GREEDY) {   // sampling.py:47-48
         uint32_t bk = 0, bi = 0;
-        stream_row<TIn>(rowp, V, bm, pen_on, pen,
+        stream_row_pen<TIn>(rowp, V, bm, pen_on, pen,
             [&](int, int e, float x) {
                 const uint32_t g = (x != x) ? 0xFFFFFFFFu : vkey(x);   // NaN is the maximum
                 if (g > bk) { bk = g; bi = (uint32_t)e; }              // ascending e: the first maximum
@@ -1452,17 +1479,16 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
             //    sample of NSAMP logits: the lower edge of the histogram bin
             //    holding the sample's j-th largest, j well above the expected
             //    k * NSAMP / V.  It only steers the stream; step 3 checks it.
-            bool fast = V >= FAST_MIN_V;
+            bool fast = sampled;
             uint32_t est = 0;
             if (tid == 0) s_ovf = 0u;
             if (fast) {
-                constexpr int NS = NSAMP / NT;
                 const int stride = V / NT;
                 uint32_t sk4[NS], smax = 0, smin = 0xFFFFFFFFu;
 #pragma unroll
                 for (int q = 0; q < NS; ++q) {
                     const int e = tid * stride + q;
-                    float x = VecIO<TIn>::one(rowp, e);
+                    float x = sx[q];
                     if (pen_on && !defer && ((bm[e >> 5] >> (e & 31)) & 1u)) x = penalize(x, pen);
                     sk4[q] = selkey(x, neg);
                     smax = sk4[q] > smax ? sk4[q] : smax;
@@ -1471,11 +1497,9 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                 const float ks = (float)kk * (float)NSAMP / (float)V;
                 uint32_t js = (uint32_t)ceilf(ks + 6.0f * sqrtf(ks) + 3.0f);
                 js = js < (uint32_t)NSAMP ? js : (uint32_t)NSAMP;
-                const Reduced sr = block_reduce(smax, smin, 0u);
+                const Reduced sr = block_reduce(smax, smin, 0u);   // (its barriers also order the zeroed hist)
                 const uint32_t span = sr.max - sr.min;
                 const int sh = span >= 2048u ? (32 - __builtin_clz(span)) - 11 : 0;
-                for (int b = tid; b < 2048; b += NT) hist[b] = 0;
-                __syncthreads();
 #pragma unroll
                 for (int q = 0; q < NS; ++q) atomicAdd(&hist[(sk4[q] - sr.min) >> sh], 1u);
                 __syncthreads();
@@ -1496,7 +1520,7 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                 u64 wm[FPT];        // wave ballots of the hits, per slot
 #pragma unroll
                 for (int i = 0; i < FPT; ++i) wm[i] = 0;
-                stream_row<TIn>(rowp, V, bm, pen_on && !defer, pen,
+                stream_row_pen<TIn>(rowp, V, bm, pen_on && !defer, pen,
                     [&](int i, int, float x) {
                         const uint32_t sk = selkey(x, neg);
                         omax = sk > omax ? sk : omax;
@@ -1531,33 +1555,49 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                 __syncthreads();
                 fast = s_ovf == 0u;
                 if (fast) {
-                    // 3. One pass over the segments in registers: penalize the
-                    //    buffered history ids, count the keys that reach the
-                    //    estimate, and pack the segments into [0, Nc).  The
-                    //    estimate stands if at least k keys reach it (then the
-                    //    k-th largest key is >= est, and every element that
+                    // 3. Each wave reads its own segment into registers,
+                    //    penalizes its history ids and counts the keys that
+                    //    reach the estimate; after a barrier it writes them
+                    //    packed at its offset, so the buffer becomes [0, Nc).
+                    //    The estimate stands if at least k keys reach it (then
+                    //    the k-th largest key is >= est, and every element that
                     //    ties with it after x / T is >= widen(est) = theta).
-                    constexpr int PER = FCAP / NT;
-                    uint32_t kv[PER], iv[PER], nv = 0, nr = 0;
+                    constexpr int PERW = FSEG / 64;
+                    uint32_t off = 0;
+                    Nc = 0;
 #pragma unroll
-                    for (int q = 0; q < PER; ++q) {
-                        const uint32_t slot = (uint32_t)(tid + q * NT);
-                        const bool valid = (slot % FSEG) < s_seg[slot / FSEG];
-                        kv[q] = valid ? ck[slot] : 0u;
-                        iv[q] = valid ? ci[slot] : 0xFFFFFFFFu;
-                        if (valid && defer && ((bm[iv[q] >> 5] >> (iv[q] & 31)) & 1u))
-                            kv[q] = okey(penalize(okey_inv(kv[q]), pen));
-                        nv += valid ? 1u : 0u;
-                        nr += (valid && kv[q] >= est) ? 1u : 0u;
+                    for (int v = 0; v < NWAVES; ++v) {
+                        const uint32_t c = s_seg[v];
+                        off += v < w ? c : 0u;
+                        Nc += c;
                     }
-                    uint32_t tot;
-                    uint32_t o = block_incl_scan<uint32_t>(nv | (nr << 16), &tot) - (nv | (nr << 16));
-                    o &= 0xFFFFu;   // (its barriers end the reads)
+                    uint32_t kv[PERW], iv[PERW], nr = 0;
 #pragma unroll
-                    for (int q = 0; q < PER; ++q)
-                        if (iv[q] != 0xFFFFFFFFu) { ck[o] = kv[q]; ci[o] = iv[q]; ++o; }
-                    Nc = tot & 0xFFFFu;
-                    fast = (tot >> 16) >= kk;
+                    for (int q = 0; q < PERW; ++q) {
+                        const uint32_t j = (uint32_t)(lane + 64 * q);
+                        kv[q] = 0u;
+                        iv[q] = 0u;
+                        if (j < cw) {
+                            kv[q] = wck[j];
+                            iv[q] = wci[j];
+                            if (defer && ((bm[iv[q] >> 5] >> (iv[q] & 31)) & 1u))
+                                kv[q] = okey(penalize(okey_inv(kv[q]), pen));
+                            nr += kv[q] >= est ? 1u : 0u;
+                        }
+                    }
+                    uint32_t wr;
+                    (void)wave_excl_small(nr, wr);
+                    if (lane == 0) s_reach[w] = wr;
+                    __syncthreads();
+#pragma unroll
+                    for (int q = 0; q < PERW; ++q) {
+                        const uint32_t j = (uint32_t)(lane + 64 * q);
+                        if (j < cw) { ck[off + j] = kv[q]; ci[off + j] = iv[q]; }
+                    }
+                    uint32_t reach = 0;
+#pragma unroll
+                    for (int v = 0; v < NWAVES; ++v) reach += s_reach[v];
+                    fast = reach >= kk;
                     __syncthreads();
                 }
             }
@@ -1571,7 +1611,7 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                 if (tid < 3) s_cnt[tid] = 0;
                 __syncthreads();
                 uint32_t tk[FPT], te[FPT], hm = 0;   // this tile's keys, ids and hits
-                stream_row<TIn>(rowp, V, bm, pen_on && !defer, pen,
+                stream_row_pen<TIn>(rowp, V, bm, pen_on && !defer, pen,
                     [&](int i, int e, float x) {
                         const uint32_t sk = selkey(x, neg);
                         omax = sk > omax ? sk : omax;
@@ -1648,7 +1688,7 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                 if (!overflow) fix_up();
             }
         } else {
-            stream_row<TIn>(rowp, V, bm, pen_on, pen,
+            stream_row_pen<TIn>(rowp, V, bm, pen_on, pen,
                 [&](int, int, float x) {
                     const uint32_t sk = selkey(x, neg);
                     omax = sk > omax ? sk : omax;
