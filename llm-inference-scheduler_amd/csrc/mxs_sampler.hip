@@ -1376,6 +1376,247 @@ __device__ __forceinline__ uint32_t wave_excl_small(uint32_t c, uint32_t& total)
     return pre;
 }
 
+// ---------------------------------------------------------------- top-p only
+//
+// Rows with top-k off (k <= 0 or k >= V) in the fused kernel: the whole row
+// takes part in the top-p cut (sampling.py:56-66).  One pass computes every
+// element's integer mass and histograms the masses by bins linear in
+// d = l - m; the cut and the draw each find their bin by a search over the
+// mass histogram, gather that bin's elements (found by comparing selection
+// keys with the bin's key interval, so the gathering pass does no division)
+// and rank them.
+
+struct SetPick {
+    u64 key;   // (vkey << 32) | ~index
+    u64 E;     // mass before it within the set, in sorted order
+    u64 w;     // its mass
+    int ok;
+};
+
+// The element at mass position t of the sorted order (value desc, index asc)
+// of the n <= LCAP elements keys[0, n) (vkey(l) << 32 | ~index); masses are
+// mass_of(l - m).  Sub-bins linear in d over the set's range; a sub-bin of
+// more than 64 elements falls back to sorting the set in place.
+__device__ __forceinline__ SetPick pick_in_set(u64* keys, int n, u64 t, float m, u64* SMH, uint32_t* SCH)
+{
+    __shared__ u64 q_key[64], q_w[64];
+    __shared__ uint32_t q_n;
+    __shared__ SetPick q_pick;
+    const int tid = threadIdx.x;
+    uint32_t vmax = 0, vmin = 0xFFFFFFFFu;
+    for (int j = tid; j < n; j += NT) {
+        const uint32_t vk = (uint32_t)(keys[j] >> 32);
+        vmax = vk > vmax ? vk : vmax;
+        vmin = vk < vmin ? vk : vmin;
+    }
+    const Reduced rd = block_reduce(vmax, vmin, 0u);
+    const float dmin = okey_inv(rd.min) - m, dmax = okey_inv(rd.max) - m;
+    float scale = dmax > dmin ? 2047.0f / (dmax - dmin) : 0.0f;
+    if (!__builtin_isfinite(scale) || !(dmin > -INFINITY)) scale = 0.0f;
+    auto sbin = [&](uint32_t vk) -> uint32_t {
+        const float f = ((okey_inv(vk) - m) - dmin) * scale;
+        return f > 0.0f ? (f < 2047.0f ? (uint32_t)f : 2047u) : 0u;
+    };
+    for (int b = tid; b < 2048; b += NT) { SMH[b] = 0; SCH[b] = 0; }
+    if (tid == 0) { q_n = 0; q_pick = SetPick{0, 0, 0, 0}; }
+    __syncthreads();
+    for (int j = tid; j < n; j += NT) {
+        const uint32_t vk = (uint32_t)(keys[j] >> 32);
+        const uint32_t b = sbin(vk);
+        atomicAdd(&SMH[b], mass_of(okey_inv(vk) - m));
+        atomicAdd(&SCH[b], 1u);
+    }
+    __syncthreads();
+    const BinHit hit = find_desc<u64>(SMH, 2048, t);
+    const uint32_t cnt = SCH[hit.bin];
+    if (cnt <= 64u) {
+        for (int j = tid; j < n; j += NT) {
+            const u64 key = keys[j];
+            if (sbin((uint32_t)(key >> 32)) == (uint32_t)hit.bin) {
+                const uint32_t slot = atomicAdd(&q_n, 1u);
+                if (slot < 64u) { q_key[slot] = key; q_w[slot] = mass_of(okey_inv((uint32_t)(key >> 32)) - m); }
+            }
+        }
+        __syncthreads();
+        if (wave_id() == 0) {
+            const uint32_t lane = (uint32_t)lane_id();
+            const uint32_t c = q_n < 64u ? q_n : 64u;
+            const u64 mk = lane < c ? q_key[lane] : 0ull;
+            const u64 mw = lane < c ? q_w[lane] : 0ull;
+            u64 before = 0;
+            for (uint32_t q = 0; q < c; ++q) before += q_key[q] > mk ? q_w[q] : 0ull;
+            const u64 E = hit.above + before;
+            if (lane < c && E <= t && t < E + mw) q_pick = SetPick{mk, E, mw, 1};
+        }
+        __syncthreads();
+        const SetPick res = q_pick;
+        __syncthreads();
+        return res;
+    }
+    // heavy ties: sort the set (descending) and scan its masses
+    __syncthreads();
+    const int P = pow2_ceil(n);
+    for (int j = n + tid; j < P; j += NT) keys[j] = 0;
+    __syncthreads();
+    bitonic_sort_desc(keys, P);
+    constexpr int PER = LCAP / NT;
+    const int j0 = tid * PER;
+    u64 wv[PER], run = 0;
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+        const int j = j0 + q;
+        wv[q] = j < n ? mass_of(okey_inv((uint32_t)(keys[j] >> 32)) - m) : 0ull;
+        run += wv[q];
+    }
+    u64 tot;
+    u64 E = block_incl_scan<u64>(run, &tot) - run;
+    if (tid == 0) q_pick = SetPick{0, 0, 0, 0};
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+        const int j = j0 + q;
+        if (j < n && E <= t && t < E + wv[q]) q_pick = SetPick{keys[j], E, wv[q], 1};
+        E += wv[q];
+    }
+    __syncthreads();
+    const SetPick res = q_pick;
+    __syncthreads();
+    return res;
+}
+
+// Smallest s in [lo, hi] with pred(s), for pred monotone (false, then true)
+// and pred(hi) true; called by a whole wave, 64 probes per step.
+template <class Pred>
+__device__ __forceinline__ uint32_t wave_first_true(uint32_t lo, uint32_t hi, Pred pred)
+{
+    const uint32_t lane = (uint32_t)lane_id();
+    while (lo < hi) {
+        const u64 span = (u64)(hi - lo);
+        const uint32_t pt = lo + (uint32_t)((span * (lane + 1u)) >> 6);   // lane 63 probes hi
+        const u64 msk = __ballot(pred(pt));
+        const int f = __builtin_ctzll(msk);
+        const uint32_t nhi = (uint32_t)__builtin_amdgcn_readlane((int)pt, f);
+        const uint32_t nlo = f > 0 ? (uint32_t)__builtin_amdgcn_readlane((int)pt, f - 1) + 1u : lo;
+        lo = nlo;
+        hi = nhi;
+    }
+    return lo;
+}
+
+// Top-p cut and draw over a whole row (top-k off).  skmax / skmin: the
+// largest and smallest selection keys of the penalized row.  Returns false
+// when a bin holds more than LCAP elements (the caller's multi-level path
+// takes over).
+template <typename TIn>
+__device__ __forceinline__ bool finish_wide(const Params& p, int r, float T, bool neg, float top_p, float u, float pen,
+                                            bool pen_on, const uint32_t* bm, uint32_t skmax, uint32_t skmin, u64* MH,
+                                            uint32_t* CH, u64* keys, u64* SMH, uint32_t* SCH, int64_t& tok,
+                                            int32_t& st)
+{
+    __shared__ uint32_t g_sa, g_sb, g_cnt;
+    const int tid = threadIdx.x;
+    const int V = p.V;
+    const TIn* rowp = (const TIn*)p.logits + (size_t)r * (size_t)p.ld;
+    const float m = sel_inv(skmax, neg) / T;
+    if (!isfinite(m)) { st = MXS_ROW_NONFINITE; tok = -1; return true; }
+    float dlo = sel_inv(skmin, neg) / T - m;
+    if (!(dlo > -104.0f)) dlo = -104.0f;   // masses below are zero
+    float scale = dlo < 0.0f ? 2047.0f / -dlo : 0.0f;
+    if (!__builtin_isfinite(scale)) scale = 0.0f;
+    auto bin_of = [&](float d) -> uint32_t {   // monotone in d
+        const float f = (d - dlo) * scale;
+        return f > 0.0f ? (f < 2047.0f ? (uint32_t)f : 2047u) : 0u;
+    };
+
+    // sampling.py:57-59: every element's mass, histogrammed by bin
+    for (int b = tid; b < 2048; b += NT) { MH[b] = 0; CH[b] = 0; }
+    __syncthreads();
+    u64 wsum = 0;
+    stream_row_pen<TIn>(rowp, V, bm, pen_on, pen,
+        [&](int, int, float x) {
+            const float l = x / T;
+            const float d = l - m;
+            const u64 w = mass_of(d);
+            const uint32_t b = bin_of(d);
+            atomicAdd(&MH[b], w);
+            atomicAdd(&CH[b], 1u);
+            wsum += w;
+        },
+        [&](auto&&) { return false; });
+    const u64 W = block_sum<u64>(wsum);   // (its barriers publish the histograms)
+
+    // bin b's elements (vkey(l) << 32 | ~index) into keys; -1 if more than LCAP
+    auto gather_bin = [&](uint32_t b) -> int {
+        if (wave_id() == 0) {
+            auto bin_of_key = [&](uint32_t sk) { return bin_of(sel_inv(sk, neg) / T - m); };
+            const uint32_t KHI = 0xFF800000u;   // selection keys of real values: [SK_MIN, KHI]
+            const uint32_t sa = wave_first_true(SK_MIN, KHI, [&](uint32_t sk) { return bin_of_key(sk) >= b; });
+            const uint32_t sb = b >= 2047u ? KHI
+                : wave_first_true(SK_MIN, KHI, [&](uint32_t sk) { return bin_of_key(sk) >= b + 1u; }) - 1u;
+            if (lane_id() == 0) { g_sa = sa; g_sb = sb; g_cnt = 0; }
+        }
+        __syncthreads();
+        const uint32_t sa = g_sa, sb = g_sb;
+        stream_row_pen<TIn>(rowp, V, bm, pen_on, pen,
+            [&](int, int e, float x) {
+                const uint32_t sk = selkey(x, neg);
+                if (sk >= sa && sk <= sb) {
+                    const uint32_t slot = atomicAdd(&g_cnt, 1u);
+                    if (slot < (uint32_t)LCAP)
+                        keys[slot] = ((u64)vkey(x / T) << 32) | (u64)(0xFFFFFFFFu - (uint32_t)e);
+                }
+            },
+            [&](auto&&) { return false; });
+        __syncthreads();
+        const uint32_t n = g_cnt;
+        __syncthreads();
+        return n <= (uint32_t)LCAP ? (int)n : -1;
+    };
+
+    bool bounded = false;
+    u64 bound = 0, Wk = W, A_cut = 0;
+    int n_cut = -1;
+    if (top_p < 1.0f) {   // sampling.py:56-63
+        if (!(top_p > 0.0f)) { st = MXS_ROW_EMPTY_NUCLEUS; tok = -1; return true; }
+        const u64 t = ceil_mul(top_p, W) - 1;
+        const BinHit hc = find_desc<u64>(MH, 2048, t);
+        if (CH[hc.bin] > (uint32_t)LCAP) return false;
+        n_cut = gather_bin((uint32_t)hc.bin);
+        if (n_cut < 0) return false;
+        const SetPick c = pick_in_set(keys, n_cut, t - hc.above, m, SMH, SCH);
+        if (!c.ok) return false;
+        bounded = true;
+        bound = c.key;
+        A_cut = hc.above;
+        Wk = hc.above + c.E + c.w;
+    }
+    const u64 D = floor_mul(clamp_uniform(u), Wk);   // sampling.py:69
+    SetPick dp;
+    if (n_cut >= 0 && D >= A_cut) {
+        dp = pick_in_set(keys, n_cut, D - A_cut, m, SMH, SCH);   // the cut's bin (kept part lies below Wk)
+    } else {
+        const BinHit hd = find_desc<u64>(MH, 2048, D);          // a bin wholly kept
+        if (CH[hd.bin] > (uint32_t)LCAP) return false;
+        const int n = gather_bin((uint32_t)hd.bin);
+        if (n < 0) return false;
+        dp = pick_in_set(keys, n, D - hd.above, m, SMH, SCH);
+    }
+    if (!dp.ok) return false;
+    tok = (int64_t)(0xFFFFFFFFu - (uint32_t)dp.key);
+    st = MXS_ROW_OK;
+    if (p.out_probs) {   // sampling.py:68
+        float* out = p.out_probs + (size_t)r * (size_t)V;
+        stream_row_pen<TIn>(rowp, V, bm, pen_on, pen,
+            [&](int, int e, float x) {
+                const float l = x / T;
+                const u64 key = ((u64)vkey(l) << 32) | (u64)(0xFFFFFFFFu - (uint32_t)e);
+                if (!bounded || key >= bound) out[e] = (float)((double)mass_of(l - m) / (double)Wk);
+            },
+            [&](auto&&) { return false; });
+    }
+    return true;
+}
+
 template <typename TIn>
 __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
 {
@@ -1735,6 +1976,12 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                     done = finish_kept(p, r, keys, (u64*)(smem + KF_CK), (int)n1u, top_p, u,
                                        (u64*)(smem + KF_MH), hist, tok, st);
                 }
+            }
+            if (!done && mode == MODE_LARGE && (k <= 0 || k >= V)) {
+                __syncthreads();
+                done = finish_wide<TIn>(p, r, T, neg, top_p, u, pen, pen_on, bm, rd.max, rd.min, (u64*)(smem + KF_MH),
+                                        hist, (u64*)(smem + KF_CK), (u64*)(smem + KF_CK + 8 * LCAP),
+                                        (uint32_t*)(smem + KF_CK + 8 * LCAP + 8 * 2048), tok, st);
             }
             if (!done) {
                 __syncthreads();

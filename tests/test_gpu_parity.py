@@ -224,6 +224,12 @@ def test_parity_one_workgroup_per_row_fallbacks(oracle, cuda):
     r = (2.0 * rng.standard_normal(V)).astype(np.float32)
     r[4242] = np.frombuffer(np.uint32(0xFFC00000).tobytes(), np.float32)[0]
     rows.append(r); params.append((0.9, 50, 0.9, 1.2, [4242, 7], 0.5))   # a negative NaN
+    # top-k off: the whole row takes part in the top-p cut and the draw
+    for T, kq, pq, pen, u in [(0.7, 0, 0.95, 1.05, 0.31), (1.3, 0, 0.5, 1.0, 0.77),
+                              (0.9, 0, 1.0, 1.2, 0.05), (0.8, V, 0.8, 1.0, 0.99),
+                              (-0.8, 0, 0.9, 1.1, 0.5)]:
+        r = rng.standard_normal(V).astype(np.float32)
+        rows.append(r); params.append((T, kq, pq, pen, list(range(3, V, 71)), u))
     z = make_workload("zipf", B=128 - len(rows))
     x = np.concatenate([np.stack(rows), z.logits])
     T = [p[0] for p in params] + z.temperature.tolist()
