@@ -49,6 +49,8 @@ constexpr int NSAMP = 2048;                     // logits sampled for the first 
 constexpr int FAST_MIN_V = 8 * NSAMP;           // rows shorter than this skip the sample
 constexpr int KF_CK = 0;                        // FCAP candidate keys; later SORT_CAP masses
 constexpr int KF_CI = KF_CK + 4 * FCAP;         // FCAP candidate ids
+constexpr int KF_HL = 90112;                    // top-k-off rows: distinct history ids (in the candidate area)
+constexpr int HCAP = (2 * 4 * FCAP - KF_HL) / 4; // 2048 of them
 constexpr int KF_BM = KF_CI + 4 * FCAP;         // history bitmap (MXS_MAX_VOCAB bits); later sort keys
 constexpr int KF_MH = KF_BM + 32768;            // 2048 x u64
 constexpr int KF_H = KF_MH + 16384;             // 2048 x u32

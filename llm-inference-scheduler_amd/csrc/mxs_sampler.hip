@@ -1504,16 +1504,18 @@ __device__ __forceinline__ uint32_t wave_first_true(uint32_t lo, uint32_t hi, Pr
 }
 
 // Top-p cut and draw over a whole row (top-k off).  skmax / skmin: the
-// largest and smallest selection keys of the penalized row.  Returns false
-// when a bin holds more than LCAP elements (the caller's multi-level path
-// takes over).
+// largest and smallest selection keys of the penalized row.  The passes here
+// read raw values; the history ids (each once, from the bitmap) are then
+// corrected to their penalized values, so no pass branches on the penalty
+// per element.  Returns false when a bin holds more than LCAP elements (the
+// caller's multi-level path takes over).
 template <typename TIn>
 __device__ __forceinline__ bool finish_wide(const Params& p, int r, float T, bool neg, float top_p, float u, float pen,
-                                            bool pen_on, const uint32_t* bm, uint32_t skmax, uint32_t skmin, u64* MH,
-                                            uint32_t* CH, u64* keys, u64* SMH, uint32_t* SCH, int64_t& tok,
-                                            int32_t& st)
+                                            bool pen_on, const uint32_t* bm, const uint32_t* hl, uint32_t nh,
+                                            uint32_t skmax, uint32_t skmin, u64* MH, uint32_t* CH, u64* keys_c,
+                                            u64* keys_d, u64* SMH, uint32_t* SCH, int64_t& tok, int32_t& st)
 {
-    __shared__ uint32_t g_sa, g_sb, g_cnt;
+    __shared__ uint32_t g_iv[4], g_cnt[2];
     const int tid = threadIdx.x;
     const int V = p.V;
     const TIn* rowp = (const TIn*)p.logits + (size_t)r * (size_t)p.ld;
@@ -1527,12 +1529,43 @@ __device__ __forceinline__ bool finish_wide(const Params& p, int r, float T, boo
         const float f = (d - dlo) * scale;
         return f > 0.0f ? (f < 2047.0f ? (uint32_t)f : 2047u) : 0u;
     };
+    // f(id, raw value) for every history id once: from the list (loads four
+    // at a time), or from the bitmap's set bits if the list overflowed
+    auto for_history = [&](auto&& f) {
+        if (nh <= (uint32_t)HCAP) {
+            for (uint32_t i0 = tid; i0 < nh; i0 += 4 * NT) {
+                int id[4];
+                float xv[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const uint32_t i = i0 + (uint32_t)(q * NT);
+                    id[q] = i < nh ? (int)hl[i] : -1;
+                }
+#pragma unroll
+                for (int q = 0; q < 4; ++q) xv[q] = id[q] >= 0 ? VecIO<TIn>::one(rowp, id[q]) : 0.0f;
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    if (id[q] >= 0) f(id[q], xv[q]);
+            }
+        } else {
+            const int words = (V + 31) >> 5;
+            for (int wd = tid; wd < words; wd += NT) {
+                uint32_t bits = bm[wd];
+                while (bits) {
+                    const int bi = __builtin_ctz(bits);
+                    bits &= bits - 1u;
+                    f(wd * 32 + bi, VecIO<TIn>::one(rowp, wd * 32 + bi));
+                }
+            }
+        }
+    };
+    auto is_history = [&](int e) { return ((bm[e >> 5] >> (e & 31)) & 1u) != 0u; };
 
     // sampling.py:57-59: every element's mass, histogrammed by bin
     for (int b = tid; b < 2048; b += NT) { MH[b] = 0; CH[b] = 0; }
     __syncthreads();
     u64 wsum = 0;
-    stream_row_pen<TIn>(rowp, V, bm, pen_on, pen,
+    stream_row<TIn, false>(rowp, V, bm, pen,
         [&](int, int, float x) {
             const float l = x / T;
             const float d = l - m;
@@ -1543,63 +1576,108 @@ __device__ __forceinline__ bool finish_wide(const Params& p, int r, float T, boo
             wsum += w;
         },
         [&](auto&&) { return false; });
+    if (pen_on) {   // the history ids: raw contribution out, penalized one in
+        for_history([&](int, float x) {
+            const float d0 = x / T - m, d1 = penalize(x, pen) / T - m;
+            const u64 w0 = mass_of(d0), w1 = mass_of(d1);
+            atomicAdd(&MH[bin_of(d0)], 0ull - w0);
+            atomicAdd(&CH[bin_of(d0)], 0xFFFFFFFFu);
+            atomicAdd(&MH[bin_of(d1)], w1);
+            atomicAdd(&CH[bin_of(d1)], 1u);
+            wsum += w1 - w0;
+        });
+    }
     const u64 W = block_sum<u64>(wsum);   // (its barriers publish the histograms)
 
-    // bin b's elements (vkey(l) << 32 | ~index) into keys; -1 if more than LCAP
-    auto gather_bin = [&](uint32_t b) -> int {
+    // The elements of bins bc and bd (bd < 0: none) into keys_c / keys_d as
+    // (vkey(l) << 32 | ~index), found by comparing selection keys with each
+    // bin's key interval.  Returns false if a set exceeds LCAP.
+    auto gather = [&](int bc, int bd) -> bool {
         if (wave_id() == 0) {
-            auto bin_of_key = [&](uint32_t sk) { return bin_of(sel_inv(sk, neg) / T - m); };
             const uint32_t KHI = 0xFF800000u;   // selection keys of real values: [SK_MIN, KHI]
-            const uint32_t sa = wave_first_true(SK_MIN, KHI, [&](uint32_t sk) { return bin_of_key(sk) >= b; });
-            const uint32_t sb = b >= 2047u ? KHI
-                : wave_first_true(SK_MIN, KHI, [&](uint32_t sk) { return bin_of_key(sk) >= b + 1u; }) - 1u;
-            if (lane_id() == 0) { g_sa = sa; g_sb = sb; g_cnt = 0; }
+            auto first_at_least = [&](uint32_t b) -> uint32_t {
+                if (b > 2047u) return KHI + 1u;
+                return wave_first_true(SK_MIN, KHI, [&](uint32_t sk) { return bin_of(sel_inv(sk, neg) / T - m) >= b; });
+            };
+            const uint32_t ca = first_at_least((uint32_t)bc), cb = first_at_least((uint32_t)bc + 1u) - 1u;
+            uint32_t da = 1u, db = 0u;   // empty
+            if (bd >= 0) { da = first_at_least((uint32_t)bd); db = first_at_least((uint32_t)bd + 1u) - 1u; }
+            if (lane_id() == 0) { g_iv[0] = ca; g_iv[1] = cb; g_iv[2] = da; g_iv[3] = db; g_cnt[0] = 0; g_cnt[1] = 0; }
         }
         __syncthreads();
-        const uint32_t sa = g_sa, sb = g_sb;
-        stream_row_pen<TIn>(rowp, V, bm, pen_on, pen,
+        const uint32_t ca = g_iv[0], cb = g_iv[1], da = g_iv[2], db = g_iv[3];
+        auto put = [&](uint32_t sk, float x, int e) {
+            const u64 key = ((u64)vkey(x / T) << 32) | (u64)(0xFFFFFFFFu - (uint32_t)e);
+            if (sk >= ca && sk <= cb) {
+                const uint32_t slot = atomicAdd(&g_cnt[0], 1u);
+                if (slot < (uint32_t)LCAP) keys_c[slot] = key;
+            } else if (sk >= da && sk <= db) {
+                const uint32_t slot = atomicAdd(&g_cnt[1], 1u);
+                if (slot < (uint32_t)LCAP) keys_d[slot] = key;
+            }
+        };
+        stream_row<TIn, false>(rowp, V, bm, pen,
             [&](int, int e, float x) {
                 const uint32_t sk = selkey(x, neg);
-                if (sk >= sa && sk <= sb) {
-                    const uint32_t slot = atomicAdd(&g_cnt, 1u);
-                    if (slot < (uint32_t)LCAP)
-                        keys[slot] = ((u64)vkey(x / T) << 32) | (u64)(0xFFFFFFFFu - (uint32_t)e);
+                if ((sk >= ca && sk <= cb) || (sk >= da && sk <= db)) {
+                    if (!(pen_on && is_history(e))) put(sk, x, e);
                 }
             },
             [&](auto&&) { return false; });
+        if (pen_on) {
+            for_history([&](int e, float x0) {
+                const float x = penalize(x0, pen);
+                put(selkey(x, neg), x, e);
+            });
+        }
         __syncthreads();
-        const uint32_t n = g_cnt;
-        __syncthreads();
-        return n <= (uint32_t)LCAP ? (int)n : -1;
+        const bool ok = g_cnt[0] <= (uint32_t)LCAP && g_cnt[1] <= (uint32_t)LCAP;
+        return ok;
     };
 
     bool bounded = false;
-    u64 bound = 0, Wk = W, A_cut = 0;
-    int n_cut = -1;
+    u64 bound = 0, Wk = W;
+    SetPick dp{0, 0, 0, 0};
     if (top_p < 1.0f) {   // sampling.py:56-63
         if (!(top_p > 0.0f)) { st = MXS_ROW_EMPTY_NUCLEUS; tok = -1; return true; }
         const u64 t = ceil_mul(top_p, W) - 1;
         const BinHit hc = find_desc<u64>(MH, 2048, t);
-        if (CH[hc.bin] > (uint32_t)LCAP) return false;
-        n_cut = gather_bin((uint32_t)hc.bin);
-        if (n_cut < 0) return false;
-        const SetPick c = pick_in_set(keys, n_cut, t - hc.above, m, SMH, SCH);
+        const u64 A = hc.above;
+        // where the draw can land: Wk lies in (A, A + mass of the cut's bin]
+        const u64 Dlo = floor_mul(clamp_uniform(u), A), Dhi = floor_mul(clamp_uniform(u), A + MH[hc.bin]);
+        int bd = -1;
+        if (Dhi < A) {
+            const BinHit h1 = find_desc<u64>(MH, 2048, Dlo);
+            const BinHit h2 = find_desc<u64>(MH, 2048, Dhi);
+            if (h1.bin == h2.bin) bd = h1.bin;
+        }
+        if (CH[hc.bin] > (uint32_t)LCAP || (bd >= 0 && CH[bd] > (uint32_t)LCAP)) return false;
+        if (!gather(hc.bin, bd)) return false;
+        const int nc = (int)g_cnt[0], nd = (int)g_cnt[1];
+        const SetPick c = pick_in_set(keys_c, nc, t - A, m, SMH, SCH);
         if (!c.ok) return false;
         bounded = true;
         bound = c.key;
-        A_cut = hc.above;
-        Wk = hc.above + c.E + c.w;
-    }
-    const u64 D = floor_mul(clamp_uniform(u), Wk);   // sampling.py:69
-    SetPick dp;
-    if (n_cut >= 0 && D >= A_cut) {
-        dp = pick_in_set(keys, n_cut, D - A_cut, m, SMH, SCH);   // the cut's bin (kept part lies below Wk)
+        Wk = A + c.E + c.w;
+        const u64 D = floor_mul(clamp_uniform(u), Wk);   // sampling.py:69
+        if (D >= A) {
+            dp = pick_in_set(keys_c, nc, D - A, m, SMH, SCH);   // the cut's bin (its kept part lies below Wk)
+        } else {
+            const BinHit hd = find_desc<u64>(MH, 2048, D);   // a bin above the cut's, wholly kept
+            if (hd.bin != bd) {
+                if (CH[hd.bin] > (uint32_t)LCAP) return false;
+                if (!gather(hd.bin, -1)) return false;
+                dp = pick_in_set(keys_c, (int)g_cnt[0], D - hd.above, m, SMH, SCH);
+            } else {
+                dp = pick_in_set(keys_d, nd, D - hd.above, m, SMH, SCH);
+            }
+        }
     } else {
-        const BinHit hd = find_desc<u64>(MH, 2048, D);          // a bin wholly kept
+        const u64 D = floor_mul(clamp_uniform(u), W);   // sampling.py:69
+        const BinHit hd = find_desc<u64>(MH, 2048, D);
         if (CH[hd.bin] > (uint32_t)LCAP) return false;
-        const int n = gather_bin((uint32_t)hd.bin);
-        if (n < 0) return false;
-        dp = pick_in_set(keys, n, D - hd.above, m, SMH, SCH);
+        if (!gather(hd.bin, -1)) return false;
+        dp = pick_in_set(keys_c, (int)g_cnt[0], D - hd.above, m, SMH, SCH);
     }
     if (!dp.ok) return false;
     tok = (int64_t)(0xFFFFFFFFu - (uint32_t)dp.key);
@@ -1628,6 +1706,7 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
     __shared__ uint32_t s_cnt[3];               // appends per tile, rotating
     __shared__ uint32_t s_seg[NWAVES];          // entries per buffer segment
     __shared__ uint32_t s_ovf;                  // a segment ran full
+    __shared__ uint32_t s_nh;                   // distinct history ids listed in hl
     __shared__ uint32_t s_reach[NWAVES];        // keys reaching the estimate, per segment
 
     const int tid = threadIdx.x, lane = lane_id();
@@ -1665,16 +1744,26 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
     }
     if (tid < 3) s_cnt[tid] = 0;
 
-    // sampling.py:38-45: the row's history ids, each once (sorted(set()))
+    // sampling.py:38-45: the row's history ids, each once (sorted(set())).
+    // Rows with top-k off also list them (the thread that sets an id's bit
+    // appends it) for the passes that correct raw values to penalized ones.
     bool bad = false;
+    uint32_t* hl = (uint32_t*)(smem + KF_HL);
+    if (tid == 0) s_nh = 0;
     if (pen_on) {
         const int words = (V + 31) >> 5;
         for (int w = tid; w < words; w += NT) bm[w] = 0;
         __syncthreads();
+        const bool list = mode == MODE_LARGE;
         for (int h = h0 + tid; h < h1; h += NT) {
             const int id = p.hids[h];
             if (id < 0 || id >= V) { bad = true; continue; }
-            atomicOr(&bm[id >> 5], 1u << (id & 31));
+            const uint32_t bit = 1u << (id & 31);
+            const uint32_t old = atomicOr(&bm[id >> 5], bit);
+            if (list && !(old & bit)) {
+                const uint32_t slot = atomicAdd(&s_nh, 1u);
+                if (slot < (uint32_t)HCAP) hl[slot] = (uint32_t)id;
+            }
         }
     }
     if (block_max<uint32_t>(bad ? 1u : 0u)) st = MXS_ROW_BAD_HISTORY;   // (its barriers publish bm)
@@ -1979,9 +2068,11 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
             }
             if (!done && mode == MODE_LARGE && (k <= 0 || k >= V)) {
                 __syncthreads();
-                done = finish_wide<TIn>(p, r, T, neg, top_p, u, pen, pen_on, bm, rd.max, rd.min, (u64*)(smem + KF_MH),
+                done = finish_wide<TIn>(p, r, T, neg, top_p, u, pen, pen_on, bm, hl, s_nh, rd.max, rd.min,
+                                        (u64*)(smem + KF_MH),
                                         hist, (u64*)(smem + KF_CK), (u64*)(smem + KF_CK + 8 * LCAP),
-                                        (uint32_t*)(smem + KF_CK + 8 * LCAP + 8 * 2048), tok, st);
+                                        (u64*)(smem + KF_CK + 16 * LCAP),
+                                        (uint32_t*)(smem + KF_CK + 16 * LCAP + 8 * 2048), tok, st);
             }
             if (!done) {
                 __syncthreads();
