@@ -251,7 +251,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
                      "algorithmic_bytes_per_launch": algo,
-                     "kernel": ("k_fused (one workgroup per row)" if w.B >= 128 else "k_chunks + k_rows") + ", one mxs_sample call"},
+                     "kernel": "k_fused (one workgroup per row), one mxs_sample call"},
         "cold_mall": cold,
         "parity_vs_oracle": parity,
     }

@@ -6,7 +6,7 @@
  *   -> softmax -> draw,
  * the chain of mini_engine/sampling.py:30-69, with per-row parameters passed
  * as device arrays.  Plain pointers and sizes only; every buffer belongs to
- * the caller and the library allocates nothing.  A call enqueues two kernels
+ * the caller and the library allocates nothing.  A call enqueues one kernel
  * on `stream` and returns; two calls may run concurrently only with distinct
  * workspaces.
  *
@@ -64,11 +64,11 @@ const char* mxs_version(void);
 const char* mxs_status_string(int status);
 
 /*
- * Workspace size in bytes for a batch of B rows of V logits: per-(row, chunk)
- * partial results and top-k candidate lists written by the first kernel and
- * read by the second within the same call.  It must be 256-byte aligned; it
- * needs no initialization and its contents need not survive between calls.
- * Returns 0 for an invalid shape.
+ * Workspace size in bytes for a batch of B rows of V logits.  The current
+ * kernel keeps every row's state on chip and needs only a token 256 bytes;
+ * callers size the buffer with this function so that a later version may use
+ * more.  It must be 256-byte aligned; it needs no initialization and its
+ * contents need not survive between calls.  Returns 0 for an invalid shape.
  */
 size_t mxs_workspace_bytes(int B, int V);
 

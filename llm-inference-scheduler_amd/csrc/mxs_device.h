@@ -17,29 +17,11 @@ typedef unsigned __int128 u128;
 
 constexpr int NT = 512;                 // threads per workgroup
 constexpr int NWAVES = NT / 64;
-constexpr int CS_MAX = 16384;           // logits staged in LDS per chunk
-constexpr int CS_MIN = 2048;
-constexpr int NC_MAX = 255;             // chunks per row
 constexpr int KMAX = 1024;              // largest top_k served by the candidate path
-constexpr int CHUNK_CAP = 4096;         // candidates one chunk may emit
-constexpr int CAND_LDS = 16384;         // candidate keys the finisher keeps in LDS
 constexpr int SORT_CAP = 4096;          // top-k survivors sorted in LDS (= 8 per thread)
 constexpr int LCAP = 4096;              // elements collected per refinement step (= 8 per thread)
 constexpr int MASS_SHIFT = 20;          // masses carry 44 fractional bits: 24-bit P << (20 + n)
 constexpr uint32_t SK_MIN = 0x007FFFFFu;  // selection key of -inf (T > 0) or +inf (T < 0)
-
-// LDS map of the chunk kernel (dynamic shared memory).
-constexpr int K1_KS = 0;                        // 8 * NT group-extreme keys
-constexpr int K1_HIST = K1_KS + 32 * NT;        // 2048 x u32 histogram
-constexpr int K1_BM = K1_HIST + 8192;           // CS_MAX bits of history bitmap
-constexpr int K1_LDS_BYTES = K1_BM + CS_MAX / 8;
-
-// LDS map of the row kernel.
-constexpr int K2_A = 0;                         // 64 KB: candidate keys / row penalty bitmap
-constexpr int K2_B = 65536;                     // 64 KB: sort keys + prefix masses / histograms
-constexpr int K2_HIST = K2_B + 65536;           // 2048 x u32
-constexpr int K2_OFF = K2_HIST + 8192;          // NC_MAX + 1 candidate offsets
-constexpr int K2_LDS_BYTES = K2_OFF + 4 * (NC_MAX + 1);
 
 // LDS map of the one-workgroup-per-row kernel.
 constexpr int FCAP = 12288;                     // candidates held while streaming
@@ -144,23 +126,6 @@ __host__ __device__ __forceinline__ float clamp_uniform(float u)
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
-
-__device__ __forceinline__ u64 wave_max_u64(u64 v)
-{
-    for (int o = 32; o > 0; o >>= 1) {
-        u64 w = __shfl_xor(v, o, 64);
-        v = w > v ? w : v;
-    }
-    return v;
-}
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
-{
-    for (int o = 32; o > 0; o >>= 1) {
-        uint32_t w = __shfl_xor(v, o, 64);
-        v = w > v ? w : v;
-    }
-    return v;
-}
 
 template <typename T>
 __device__ __forceinline__ T block_max(T v)

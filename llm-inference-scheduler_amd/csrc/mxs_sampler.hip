@@ -1,28 +1,16 @@
 // mxs_sampler.hip -- gfx950 sampler chain behind the C ABI of include/mxs_sampler.h.
 //
 // Reference chain: mini_engine/sampling.py:30-69, one [vocab] row per call.
-// Here one call samples a whole [B, V] batch with two launches:
-//
-// k_chunks  grid B x NC, workgroup (r, c) owns chunk c of row r (<= 16384
-//           logits, 32 per thread).  It streams the chunk from HBM once in
-//           128-bit loads into registers (fp16 upcast to fp32 there) and marks
-//           the history ids inside the chunk in an LDS bitmap (each id once).
-//           Then per row mode:
-//             greedy  argmax of the penalized chunk as a packed (key, ~index)
-//             top-k   a lower bound on the chunk's k'-th largest raw value from
-//                     the extremes of groups of 8 (k' = k + history ids in the chunk),
-//                     widened over the rounding of x / T; the elements above it
-//                     and every history id are written, with penalized values,
-//                     to the chunk's candidate slot
-//             other   chunk maximum only
-//           Results go to fixed per-(row, chunk) slots: no atomics, no
-//           cross-workgroup waits, nothing to clear between calls.
-// k_rows    grid B, one workgroup per row, after k_chunks (the kernel boundary
-//           makes the slots visible).  Exact top-k over the candidates, bitonic
-//           sort in LDS, integer softmax masses, exact top-p cut, inverse-CDF
-//           draw.  Rows with top-k off or above KMAX (or whose candidates
-//           overflow) are resolved by multi-pass histogram refinement over the
-//           row in global memory.
+// Here one call samples a whole [B, V] batch with one launch of k_fused: one
+// workgroup per row (about 157 KB of LDS, so one row per CU), which streams
+// the row from HBM once and finishes it on chip:
+//   greedy     a packed (key, index) maximum;
+//   top-k      candidates above a sampled, then verified, lower bound on the
+//              k-th largest key, kept in LDS; exact k-th, top-p cut and draw
+//              from the candidates;
+//   top-k off  a mass pass over the row (from cache), then the cut's and the
+//              draw's bins gathered and ranked;
+// with a multi-level fallback (finish_large) for massive ties.
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 #include <stddef.h>
@@ -35,21 +23,12 @@ using namespace mxs;
 
 namespace {
 
-struct ChunkOut {          // one slot per (row, chunk), 16 bytes
-    u64 best;              // greedy: max (key << 32 | ~index); sampling rows: max selection key << 32
-    uint32_t count;        // candidates written to the chunk's slot
-    uint32_t flags;
-};
-static_assert(sizeof(ChunkOut) == 16, "ChunkOut layout");
-
-enum : uint32_t { FLAG_BAD_HISTORY = 1u, FLAG_OVERFLOW = 2u, FLAG_NAN = 4u };
 enum RowMode { MODE_GREEDY = 0, MODE_TOPK = 1, MODE_LARGE = 2, MODE_INVALID = 3 };
 
 struct Params {
     const void* logits;
     int B, V;
     long long ld;
-    int CS, NC;
     const float* T;
     const int32_t* K;
     const float* P;
@@ -60,30 +39,7 @@ struct Params {
     int64_t* out_tok;
     int32_t* out_status;
     float* out_probs;
-    ChunkOut* parts;       // [B * NC]
-    uint32_t* cand_sk;     // [B * NC * CHUNK_CAP] selection keys
-    uint32_t* cand_idx;    // [B * NC * CHUNK_CAP] token ids
 };
-
-struct Geometry {
-    int NC, CS;
-};
-
-Geometry geometry(int B, int V)
-{
-    const int target_wgs = 2048;
-    auto cdiv = [](long long a, long long b) { return (int)((a + b - 1) / b); };
-    int nc_min = cdiv(V, CS_MAX);
-    int nc_max = cdiv(V, CS_MIN);
-    if (nc_max > NC_MAX) nc_max = NC_MAX;
-    int want = cdiv(target_wgs, B > 0 ? B : 1);
-    int NC = want < nc_max ? want : nc_max;
-    if (NC < nc_min) NC = nc_min;
-    if (NC < 1) NC = 1;
-    int CS = cdiv(cdiv(V, NC), 8) * 8;
-    NC = cdiv(V, CS);
-    return Geometry{NC, CS};
-}
 
 __device__ __forceinline__ RowMode classify(float T, int k, int V)
 {
@@ -170,8 +126,6 @@ __device__ __forceinline__ uint32_t widen_threshold(uint32_t th, float T, bool n
     return r;
 }
 
-// ================================================================ k_chunks
-
 struct Reduced {
     uint32_t max, min, any;
 };
@@ -199,293 +153,7 @@ __device__ __forceinline__ Reduced block_reduce(uint32_t a, uint32_t b, uint32_t
     return r;
 }
 
-// The r-th largest (0-based) of the cb <= 64 keys of ks[0 .. G*NT) that fall
-// in histogram bin `bin` ((key - lo) >> sh == bin): gathered into one wave and
-// ranked by shuffles.  `fallback` is returned if the gather disagrees.
-template <int G>
-__device__ __forceinline__ uint32_t exact_in_bin(const uint32_t* ks, uint32_t lo, int sh, uint32_t bin, uint32_t cb,
-                                 uint32_t r, uint32_t fallback)
-{
-    __shared__ uint32_t s_keys[64];
-    __shared__ uint32_t s_n, s_res;
-    if (threadIdx.x == 0) { s_n = 0; s_res = fallback; }
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < G; ++i) {
-        const uint32_t key = ks[G * threadIdx.x + i];
-        if (key >= lo && ((key - lo) >> sh) == bin) {
-            const uint32_t o = atomicAdd(&s_n, 1u);
-            if (o < 64u) s_keys[o] = key;
-        }
-    }
-    __syncthreads();
-    if (wave_id() == 0 && s_n == cb) {
-        const uint32_t lane = (uint32_t)lane_id();
-        const uint32_t mine = lane < cb ? s_keys[lane] : 0u;
-        uint32_t gt = 0, ge = 0;
-        for (uint32_t t = 0; t < cb; ++t) {   // broadcast reads of the gathered keys
-            const uint32_t o = s_keys[t];
-            gt += o > mine ? 1u : 0u;
-            ge += o >= mine ? 1u : 0u;
-        }
-        const bool hit = lane < cb && gt <= r && r < ge;
-        const u64 mask = __ballot(hit);
-        if (mask && lane == (uint32_t)__builtin_ctzll(mask)) s_res = mine;
-    }
-    __syncthreads();
-    const uint32_t res = s_res;
-    __syncthreads();
-    return res;
-}
-
-constexpr int EPT = CS_MAX / NT;   // logits per thread per chunk (32)
-
-// Chunk element (j, q) of this thread: local index (tid + j*NT) * VW + q.
-template <typename TIn>
-__device__ __forceinline__ void load_chunk(const TIn* rowp, int e0, int n, float pad, float (&x)[EPT])
-{
-    typedef VecIO<TIn> IO;
-    constexpr int VW = IO::W;
-    constexpr int MAXV = EPT / VW;
-    const int tid = threadIdx.x;
-    // 128-bit loads when the chunk start is 16-byte aligned (every chunk of a
-    // row whose start is: CS is a multiple of 8 elements), scalar otherwise.
-    const bool vec_ok = (((uintptr_t)(rowp + e0)) & 15u) == 0;
-    const int nvec = vec_ok ? n / VW : 0;
-    const typename IO::vec_t* src = (const typename IO::vec_t*)(rowp + e0);
-    typename IO::vec_t regs[MAXV];
-#pragma unroll
-    for (int j = 0; j < MAXV; ++j) {
-        const int v = tid + j * NT;
-        regs[j] = typename IO::vec_t{};
-        if (v < nvec) regs[j] = src[v];
-    }
-#pragma unroll
-    for (int j = 0; j < MAXV; ++j) {
-        const int v = tid + j * NT;
-        if (v < nvec) {
-            IO::unpack(regs[j], &x[j * VW]);
-        } else {
-#pragma unroll
-            for (int q = 0; q < VW; ++q) {
-                const int e = v * VW + q;
-                x[j * VW + q] = e < n ? IO::one(rowp, e0 + e) : pad;
-            }
-        }
-    }
-}
-
-template <typename TIn>
-__global__ __launch_bounds__(NT, 2) void k_chunks(Params p)
-{
-    extern __shared__ __align__(16) unsigned char smem[];
-    uint32_t* ks = (uint32_t*)(smem + K1_KS);      // 4 * NT per-thread group keys
-    uint32_t* hist = (uint32_t*)(smem + K1_HIST);  // 2048 bins
-    uint32_t* bm = (uint32_t*)(smem + K1_BM);      // CS_MAX bits
-
-    typedef VecIO<TIn> IO;
-    constexpr int VW = IO::W;
-    constexpr int MAXV = EPT / VW;
-    const int tid = threadIdx.x;
-    const int r = blockIdx.x / p.NC;
-    const int c = blockIdx.x - r * p.NC;
-    const int V = p.V;
-    const float T = p.T[r];
-    const int k = p.K[r];
-    const float pen = p.PEN[r];
-    const RowMode mode = classify(T, k, V);
-    const bool neg = T < 0.0f;
-    const int e0 = c * p.CS;
-    const int e1 = (e0 + p.CS < V) ? e0 + p.CS : V;
-    const int n = e1 - e0;
-    const TIn* rowp = (const TIn*)p.logits + (size_t)r * (size_t)p.ld;
-    const int h0 = p.hoff ? p.hoff[r] : 0;
-    const int h1 = p.hoff ? p.hoff[r + 1] : 0;
-    const bool pen_on = (pen != 1.0f) && (h1 > h0);
-    const size_t slot = (size_t)blockIdx.x;
-    auto local = [&](int j, int q) { return (tid + j * NT) * VW + q; };
-
-    if (p.out_probs) {
-        float* o = p.out_probs + (size_t)r * (size_t)V;
-        for (int i = e0 + tid; i < e1; i += NT) o[i] = 0.0f;
-    }
-
-    float x[EPT];
-    load_chunk<TIn>(rowp, e0, n, neg ? INFINITY : -INFINITY, x);   // padding is never selected
-
-    // ---- history ids inside the chunk, once each (sampling.py:39 sorted(set()))
-    uint32_t flags = 0;
-    uint32_t hc = 0;   // distinct history ids in this chunk
-    if (pen_on) {
-        bm[tid] = 0;   // NT words = CS_MAX bits
-        __syncthreads();
-        bool bad = false;
-        for (int h = h0 + tid; h < h1; h += NT) {
-            int id = p.hids[h];
-            if (id < 0 || id >= V) { bad = true; continue; }
-            if (id >= e0 && id < e1) {
-                int o = id - e0;
-                atomicOr(&bm[o >> 5], 1u << (o & 31));
-            }
-        }
-        __syncthreads();
-        hc = block_sum<uint32_t>((uint32_t)__builtin_popcount(bm[tid]));
-        if (block_max<uint32_t>(bad ? 1u : 0u)) flags |= FLAG_BAD_HISTORY;
-    }
-
-    // bit i of hm: element x[i] of this thread is a history id
-    uint32_t hm = 0;
-    if (pen_on) {
-#pragma unroll
-        for (int j = 0; j < MAXV; ++j) {
-            const int eb = local(j, 0);
-            hm |= ((bm[eb >> 5] >> (eb & 31)) & ((1u << VW) - 1u)) << (j * VW);
-        }
-    }
-
-    u64 best = 0;
-    uint32_t count = 0;
-    if (mode == MODE_GREEDY) {   // sampling.py:45-48: argmax of the penalized row
-        if (hm) {
-#pragma unroll
-            for (int i = 0; i < EPT; ++i)
-                if ((hm >> i) & 1u) x[i] = penalize(x[i], pen);
-        }
-        uint32_t bk = 0, bi = 0;
-#pragma unroll
-        for (int j = 0; j < MAXV; ++j)
-#pragma unroll
-            for (int q = 0; q < VW; ++q) {
-                const int e = local(j, q);
-                const float v = x[j * VW + q];
-                const uint32_t g = (v != v) ? 0xFFFFFFFFu : vkey(v);
-                if (e < n && g > bk) { bk = g; bi = (uint32_t)e; }   // ascending e: first max wins
-            }
-        const u64 mine = bk ? (((u64)bk << 32) | (u64)(0xFFFFFFFFu - (uint32_t)e0 - bi)) : 0ull;
-        best = block_max<u64>(mine);
-    } else if (mode == MODE_TOPK || mode == MODE_LARGE) {
-        // NaN check: a sum of the chunk is finite unless it holds a NaN or an
-        // infinity (padding included); only then look element by element.
-        float acc = 0.0f;
-#pragma unroll
-        for (int i = 0; i < EPT; ++i) acc += x[i];
-        uint32_t nan_any = 0;
-        if (!isfinite(acc)) {
-#pragma unroll
-            for (int i = 0; i < EPT; ++i) {   // NaN after x / T: a NaN, or infinity over infinity
-                const bool real = local(i / VW, i % VW) < n;   // (padding is infinite)
-                nan_any |= ((x[i] != x[i]) || (real && __builtin_isinf(T) && __builtin_isinf(x[i]))) ? 1u : 0u;
-            }
-        }
-
-        // The extreme of each group of GS logits in the order of x / T
-        // (max for T > 0, min for T < 0); NaNs never win.
-        constexpr int GS = 4;
-        constexpr int G = EPT / GS;
-        // element x[GS*i] sits at local index group_start(i); ceil(n / GS)
-        // groups of the chunk hold at least one element
-        auto group_start = [&](int i) { return local((GS * i) / VW, (GS * i) % VW); };
-        const uint32_t groups = (uint32_t)(n + GS - 1) / GS;
-        uint32_t gk[G];
-        uint32_t gmax = 0, gmin = 0xFFFFFFFFu;
-#pragma unroll
-        for (int i = 0; i < G; ++i) {
-            float a = x[GS * i];
-            if (!neg) {
-#pragma unroll
-                for (int q = 1; q < GS; ++q) a = fmaxf(a, x[GS * i + q]);
-            } else {
-#pragma unroll
-                for (int q = 1; q < GS; ++q) a = fminf(a, x[GS * i + q]);
-            }
-            // a group of padding only holds no element: key 0, left out below
-            const bool valid = group_start(i) < n;
-            gk[i] = !valid ? 0u : ((a != a) ? SK_MIN : selkey(a, neg));
-            gmax = gk[i] > gmax ? gk[i] : gmax;
-            if (valid) gmin = gk[i] < gmin ? gk[i] : gmin;
-        }
-        const Reduced rd = block_reduce(gmax, gmin, nan_any);
-        if (rd.any) flags |= FLAG_NAN;
-        best = (u64)rd.max << 32;
-
-        if (mode == MODE_TOPK) {
-            // sampling.py:52-54.  The group extremes are values of distinct
-            // elements, so with k' = k + (history ids in the chunk) the k'-th
-            // largest of these G*NT keys bounds the chunk's k'-th largest raw
-            // key from below, and every element of the penalized top-k is a
-            // history id or at least that large.  Candidates: raw keys at or
-            // above the bound (widened over the rounding of x / T); then every
-            // history id with its raw key, in a second segment whose keys the
-            // row kernel penalizes.
-            const uint32_t kp = (uint32_t)k + hc;
-            uint32_t theta = 0;
-            if ((uint32_t)n > kp && kp <= groups) {
-#pragma unroll
-                for (int i = 0; i < G; ++i) ks[G * tid + i] = gk[i];
-                const uint32_t lo = rd.min;
-                const uint32_t span = rd.max - lo;
-                const int sh = span >= 2048u ? (32 - __builtin_clz(span)) - 11 : 0;
-                for (int b = tid; b < 2048; b += NT) hist[b] = 0;
-                __syncthreads();
-#pragma unroll
-                for (int i = 0; i < G; ++i)
-                    if (gk[i] >= lo) atomicAdd(&hist[(gk[i] - lo) >> sh], 1u);
-                __syncthreads();
-                const BinHit hit = find_desc<uint32_t>(hist, 2048, (u64)(kp - 1u));
-                uint32_t th = lo + ((uint32_t)hit.bin << sh);   // the bin's lower edge bounds it
-                const uint32_t cb = hist[hit.bin];
-                if (sh > 0 && cb <= 64u)                           // exact: rank the bin's keys
-                    th = exact_in_bin<G>(ks, lo, sh, (uint32_t)hit.bin, cb, kp - 1u - (uint32_t)hit.above, th);
-                if (th < SK_MIN) th = SK_MIN;
-                theta = widen_threshold(th, T, neg);
-            }
-            uint32_t cm = 0;   // raw candidates among my elements
-            if (theta <= SK_MIN) {   // the whole chunk
-#pragma unroll
-                for (int j = 0; j < MAXV; ++j)
-#pragma unroll
-                    for (int q = 0; q < VW; ++q)
-                        cm |= (local(j, q) < n ? 1u : 0u) << (j * VW + q);
-            } else if (!neg) {
-                const float xth = sel_inv(theta, false);
-#pragma unroll
-                for (int i = 0; i < EPT; ++i) cm |= (x[i] >= xth ? 1u : 0u) << i;
-            } else {
-                const float xth = sel_inv(theta, true);
-#pragma unroll
-                for (int i = 0; i < EPT; ++i) cm |= (x[i] <= xth ? 1u : 0u) << i;
-            }
-            const uint32_t emit = cm | hm;
-            const uint32_t c1 = (uint32_t)__builtin_popcount(cm & ~hm);
-            const uint32_t c2 = (uint32_t)__builtin_popcount(hm);
-            uint32_t tot;
-            const uint32_t pre = block_incl_scan<uint32_t>(c1 | (c2 << 16), &tot) - (c1 | (c2 << 16));
-            const uint32_t C1 = tot & 0xFFFFu, C2 = tot >> 16;
-            if (C1 + C2 > (uint32_t)CHUNK_CAP) {
-                flags |= FLAG_OVERFLOW;
-            } else {
-                count = C1 | (C2 << 16);
-                uint32_t o1 = pre & 0xFFFFu, o2 = C1 + (pre >> 16);
-                uint32_t* dsk = p.cand_sk + slot * CHUNK_CAP;
-                uint32_t* didx = p.cand_idx + slot * CHUNK_CAP;
-#pragma unroll
-                for (int j = 0; j < MAXV; ++j)
-#pragma unroll
-                    for (int q = 0; q < VW; ++q) {
-                        const int i = j * VW + q;
-                        if ((emit >> i) & 1u) {
-                            const uint32_t o = ((hm >> i) & 1u) ? o2++ : o1++;
-                            dsk[o] = selkey(x[i], neg);
-                            didx[o] = (uint32_t)(e0 + local(j, q));
-                        }
-                    }
-            }
-        }
-    }
-    if (tid == 0) p.parts[slot] = ChunkOut{best, count, flags};
-}
-
-// ================================================================ k_rows
+// ================================================================ finishing a row
 
 struct Found {
     uint32_t vk;
@@ -746,41 +414,6 @@ __device__ __forceinline__ void finish_large(const Params& p, int r, float T, in
     }
 }
 
-// The r-th largest (0-based) of the keys whose value lies in [blo, bhi],
-// known to number cnt <= 64: gathered into wave 0 and ranked by shuffles.
-template <class Visit>
-__device__ __forceinline__ uint32_t rank_in_range(Visit visit, uint32_t blo, uint32_t bhi, uint32_t cnt, uint32_t r)
-{
-    __shared__ uint32_t g_keys[64];
-    __shared__ uint32_t g_n, g_res;
-    if (threadIdx.x == 0) { g_n = 0; g_res = blo; }
-    __syncthreads();
-    visit([&](uint32_t k) {
-        if (k >= blo && k <= bhi) {
-            const uint32_t slot = atomicAdd(&g_n, 1u);
-            if (slot < 64u) g_keys[slot] = k;
-        }
-    });
-    __syncthreads();
-    if (wave_id() == 0) {
-        const uint32_t lane = (uint32_t)lane_id();
-        const uint32_t n = g_n < cnt ? g_n : cnt;
-        const uint32_t mine = lane < n ? g_keys[lane] : 0u;
-        uint32_t gt = 0, ge = 0;
-        for (uint32_t t = 0; t < n; ++t) {   // broadcast reads of the gathered keys
-            const uint32_t other = g_keys[t];
-            gt += other > mine ? 1u : 0u;
-            ge += other >= mine ? 1u : 0u;
-        }
-        const u64 mask = __ballot(lane < n && gt <= r && r < ge);
-        if (mask && lane == (uint32_t)__builtin_ctzll(mask)) g_res = mine;
-    }
-    __syncthreads();
-    const uint32_t res = g_res;
-    __syncthreads();
-    return res;
-}
-
 // The value a selection key stands for, ordered like the key: x, or -x
 // when T < 0.
 __device__ __forceinline__ float sel_val(uint32_t s, bool neg)
@@ -879,14 +512,6 @@ __device__ __forceinline__ uint32_t select_exact_in(uint32_t kk, Visit visit, ui
     return lo;
 }
 
-template <class Visit>
-__device__ __forceinline__ uint32_t select_exact(uint32_t kk, Visit visit, uint32_t* hist, bool neg)
-{
-    uint32_t mx = 0, mn = 0xFFFFFFFFu;
-    visit([&](uint32_t k) { mx = k > mx ? k : mx; mn = k < mn ? k : mn; });
-    const Reduced rd = block_reduce(mx, mn, 0u);
-    return select_exact_in(kk, visit, hist, neg, rd.min, rd.max);
-}
 
 // Fallback of finish_kept for heavy ties: bitonic sort of the kept set, then
 // the prefix sums in sorted order.
@@ -1068,167 +693,6 @@ __device__ __forceinline__ bool finish_kept(const Params& p, int r, u64* keys, u
                 out[0xFFFFFFFFu - (uint32_t)keys[j]] = (float)((double)wm[j] / (double)Wk);
     }
     return true;
-}
-
-// Top-k rows.  The chunks' candidates hold every element whose tempered
-// value reaches the row's k-th largest.  Returns false when the survivors do
-// not fit the LDS sort; the caller then takes the multi-pass path.
-//
-// Each thread owns a slice of one chunk's candidate slot (NT / NC threads per
-// chunk) and moves it in unrolled batches, so a batch costs one memory round
-// trip rather than one per element.
-template <bool IN_LDS>
-__device__ __forceinline__ bool finish_topk(const Params& p, int r, float T, int k, float top_p, float pen, float u,
-                            const uint32_t* counts, const uint32_t* off,
-                            int64_t& tok, int32_t& st)
-{
-    extern __shared__ __align__(16) unsigned char smem[];
-    uint32_t* ck = (uint32_t*)(smem + K2_A);          // CAND_LDS candidate keys
-    u64* keys = (u64*)(smem + K2_B);                  // SORT_CAP sort keys
-    u64* cum = (u64*)(smem + K2_B + 8 * SORT_CAP);    // SORT_CAP prefix masses
-    uint32_t* hist = (uint32_t*)(smem + K2_HIST);
-    constexpr int BATCH = 16;
-    const int NC = p.NC, V = p.V;
-    const bool neg = T < 0.0f;
-    const uint32_t kk = (uint32_t)(k < V ? k : V);
-    const int tpc = NT / NC;
-    const int mc = threadIdx.x / tpc;                 // my chunk (>= NC: idle)
-    const int ml = threadIdx.x - mc * tpc;            // my lane within it
-    const bool active = mc < NC;
-    // a chunk's slot holds its raw candidates, then its history ids with raw
-    // keys: those get the penalty (sampling.py:42-45) here
-    const int mc1 = active ? (int)(counts[mc] & 0xFFFFu) : 0;
-    const int mcnt = active ? mc1 + (int)(counts[mc] >> 16) : 0;
-    auto penalized = [&](uint32_t sk) -> uint32_t { return selkey(penalize(sel_inv(sk, neg), pen), neg); };
-    const size_t mslot = ((size_t)r * NC + (active ? mc : 0)) * CHUNK_CAP;
-    const uint32_t* gsk = p.cand_sk + mslot;
-    const uint32_t* gidx = p.cand_idx + mslot;
-    uint32_t* mck = ck + (active ? off[mc] : 0);
-
-    if (IN_LDS) {
-        for (int j0 = ml; j0 < mcnt; j0 += BATCH * tpc) {
-            uint32_t v[BATCH];
-#pragma unroll
-            for (int b = 0; b < BATCH; ++b) {
-                const int j = j0 + b * tpc;
-                v[b] = j < mcnt ? gsk[j] : 0u;
-            }
-#pragma unroll
-            for (int b = 0; b < BATCH; ++b) {
-                const int j = j0 + b * tpc;
-                if (j < mcnt) mck[j] = j < mc1 ? v[b] : penalized(v[b]);
-            }
-        }
-        __syncthreads();
-    }
-    auto key_at = [&](int j) -> uint32_t {
-        if (IN_LDS) return mck[j];
-        return j < mc1 ? gsk[j] : penalized(gsk[j]);
-    };
-    auto visit = [&](auto&& f) {
-        for (int j = ml; j < mcnt; j += tpc) f(key_at(j));
-    };
-
-    // sampling.py:52-54: the k-th largest, then everything that rounds onto it
-    uint32_t sk_k = select_exact(kk, visit, hist, neg);
-    if (sk_k < SK_MIN) sk_k = SK_MIN;
-    const uint32_t theta = widen_threshold(sk_k, T, neg);
-    uint32_t mine = 0;
-    visit([&](uint32_t s) { mine += s >= theta ? 1u : 0u; });
-    uint32_t n1u;
-    uint32_t o = block_incl_scan<uint32_t>(mine, &n1u) - mine;
-    const int n1 = (int)n1u;
-    if (n1 > SORT_CAP) return false;
-
-    // survivors -> (value key << 32 | ~index); their ids come in batches
-    for (int j0 = ml; j0 < mcnt; j0 += BATCH * tpc) {
-        uint32_t sv[BATCH], iv[BATCH];
-#pragma unroll
-        for (int b = 0; b < BATCH; ++b) {   // every load of the batch in flight at once
-            const int j = j0 + b * tpc;
-            const int jc = j < mcnt ? j : 0;
-            sv[b] = j < mcnt ? key_at(j) : 0u;
-            iv[b] = gidx[jc];
-        }
-#pragma unroll
-        for (int b = 0; b < BATCH; ++b) {
-            const int j = j0 + b * tpc;
-            if (j < mcnt && sv[b] >= theta) {
-                const uint32_t vk = vkey(sel_inv(sv[b], neg) / T);
-                keys[o++] = ((u64)vk << 32) | (u64)(0xFFFFFFFFu - iv[b]);
-            }
-        }
-    }
-    __syncthreads();
-    return finish_kept(p, r, keys, cum, n1, top_p, u, (u64*)(smem + K2_A), (uint32_t*)(smem + K2_HIST), tok, st);
-}
-
-template <typename TIn>
-__global__ __launch_bounds__(NT, 1) void k_rows(Params p)
-{
-    extern __shared__ __align__(16) unsigned char smem[];
-    uint32_t* off = (uint32_t*)(smem + K2_OFF);
-    __shared__ uint32_t s_counts[NC_MAX];
-    const int tid = threadIdx.x;
-    const int r = blockIdx.x;
-    const int NC = p.NC, V = p.V;
-    const float T = p.T[r];
-    const int k = p.K[r];
-    const float pen = p.PEN[r];
-    const RowMode mode = classify(T, k, V);
-    const int h0 = p.hoff ? p.hoff[r] : 0;
-    const int h1 = p.hoff ? p.hoff[r + 1] : 0;
-    const bool pen_on = (pen != 1.0f) && (h1 > h0);
-
-    u64 best = 0;
-    uint32_t fl = 0;
-    for (int c = tid; c < NC; c += NT) {
-        ChunkOut o = p.parts[(size_t)r * NC + c];
-        best = o.best > best ? o.best : best;
-        fl |= o.flags;
-        s_counts[c] = o.count;   // raw candidates | history candidates << 16
-    }
-    best = block_max<u64>(best);
-    const uint32_t flags = block_max<uint32_t>(fl & FLAG_BAD_HISTORY) |
-                           block_max<uint32_t>(fl & FLAG_OVERFLOW) | block_max<uint32_t>(fl & FLAG_NAN);
-    if (tid == 0) {
-        uint32_t a = 0;
-        for (int c = 0; c < NC; ++c) { off[c] = a; a += (s_counts[c] & 0xFFFFu) + (s_counts[c] >> 16); }
-        off[NC] = a;
-    }
-    __syncthreads();
-    const int N = (int)off[NC];
-    const float top_p = p.P[r];
-    const float u = p.U ? p.U[r] : 0.0f;
-    int64_t tok = -1;
-    int32_t st = MXS_ROW_OK;
-
-    if (flags & FLAG_BAD_HISTORY) {
-        st = MXS_ROW_BAD_HISTORY;
-    } else if (mode == MODE_INVALID) {
-        st = MXS_ROW_BAD_PARAM;
-    } else if (mode != MODE_GREEDY && (flags & FLAG_NAN)) {
-        st = MXS_ROW_NONFINITE;    // a NaN logit: no finite maximum (sampling.py:58/68 give NaN)
-    } else if (mode == MODE_GREEDY) {
-        tok = (int64_t)(0xFFFFFFFFu - (uint32_t)best);
-        if (p.out_probs && tid == 0) p.out_probs[(size_t)r * (size_t)V + (size_t)tok] = 1.0f;
-    } else {
-        bool done = false;
-        if (mode == MODE_TOPK && !(flags & FLAG_OVERFLOW))
-            done = N <= CAND_LDS ? finish_topk<true>(p, r, T, k, top_p, pen, u, s_counts, off, tok, st)
-                                 : finish_topk<false>(p, r, T, k, top_p, pen, u, s_counts, off, tok, st);
-        if (!done) {
-            __syncthreads();
-            const LargeLds lds{(uint32_t*)(smem + K2_A), (u64*)(smem + K2_B), (u64*)(smem + K2_B),
-                               (uint32_t*)(smem + K2_HIST)};
-            finish_large<TIn>(p, r, T, k, top_p, pen, pen_on, false, (uint32_t)(best >> 32), false,
-                              false, 0u, u, lds, tok, st);
-        }
-    }
-    if (tid == 0) {
-        p.out_tok[r] = st == MXS_ROW_OK ? tok : -1;
-        if (p.out_status) p.out_status[r] = st;
-    }
 }
 
 // ================================================================ k_fused
@@ -2090,50 +1554,17 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
     }
 }
 
-inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
-
-struct Layout {
-    size_t parts, cand_sk, cand_idx, total;
-};
-
-Layout layout(int B, int V)
-{
-    Geometry g = geometry(B, V);
-    const size_t slots = (size_t)B * (size_t)g.NC;
-    Layout L;
-    L.parts = 0;
-    L.cand_sk = align256(slots * sizeof(ChunkOut));
-    L.cand_idx = L.cand_sk + align256(slots * CHUNK_CAP * sizeof(uint32_t));
-    L.total = L.cand_idx + align256(slots * CHUNK_CAP * sizeof(uint32_t));
-    return L;
-}
-
-// Batches of at least this many rows run one workgroup per row (k_fused);
-// smaller ones split rows into chunks across more workgroups.
-#ifndef MXS_FUSED_MIN_B
-#define MXS_FUSED_MIN_B 128
-#endif
+// The workspace of the C ABI: every kernel here keeps a row's state in LDS,
+// so a call needs only this token amount.
+constexpr size_t WORKSPACE_BYTES = 256;
 
 template <typename TIn>
 hipError_t launch(const Params& p, hipStream_t s)
 {
-    if (p.B >= MXS_FUSED_MIN_B) {
-        static const hipError_t a0 = hipFuncSetAttribute((const void*)k_fused<TIn>,
-                                                         hipFuncAttributeMaxDynamicSharedMemorySize, KF_LDS_BYTES);
-        (void)a0;
-        hipLaunchKernelGGL(k_fused<TIn>, dim3((unsigned)p.B), dim3(NT), KF_LDS_BYTES, s, p);
-        return hipGetLastError();
-    }
-    static const hipError_t a1 = hipFuncSetAttribute((const void*)k_chunks<TIn>,
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, K1_LDS_BYTES);
-    static const hipError_t a2 = hipFuncSetAttribute((const void*)k_rows<TIn>,
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, K2_LDS_BYTES);
-    (void)a1;
-    (void)a2;
-    hipLaunchKernelGGL(k_chunks<TIn>, dim3((unsigned)((long long)p.B * p.NC)), dim3(NT), K1_LDS_BYTES, s, p);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_rows<TIn>, dim3((unsigned)p.B), dim3(NT), K2_LDS_BYTES, s, p);
+    static const hipError_t a0 = hipFuncSetAttribute((const void*)k_fused<TIn>,
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, KF_LDS_BYTES);
+    (void)a0;
+    hipLaunchKernelGGL(k_fused<TIn>, dim3((unsigned)p.B), dim3(NT), KF_LDS_BYTES, s, p);
     return hipGetLastError();
 }
 
@@ -2159,7 +1590,7 @@ const char* mxs_status_string(int status)
 size_t mxs_workspace_bytes(int B, int V)
 {
     if (B <= 0 || V <= 0 || V > MXS_MAX_VOCAB) return 0;
-    return layout(B, V).total;
+    return WORKSPACE_BYTES;
 }
 
 int mxs_sample(const void* logits, int dtype, int B, int V, int64_t ld,
@@ -2180,17 +1611,13 @@ int mxs_sample(const void* logits, int dtype, int B, int V, int64_t ld,
     if (ld < V) return MXS_ERR_INVALID_ARGUMENT;
     const uintptr_t esize = dtype == MXS_DTYPE_F32 ? 4u : 2u;
     if (((uintptr_t)logits & (esize - 1u)) || ((uintptr_t)workspace & 255u)) return MXS_ERR_ALIGNMENT;
-    const Layout L = layout(B, V);
-    if (workspace_bytes < L.total) return MXS_ERR_WORKSPACE_TOO_SMALL;
+    if (workspace_bytes < WORKSPACE_BYTES) return MXS_ERR_WORKSPACE_TOO_SMALL;
 
-    const Geometry g = geometry(B, V);
     Params p;
     p.logits = logits;
     p.B = B;
     p.V = V;
     p.ld = ld;
-    p.CS = g.CS;
-    p.NC = g.NC;
     p.T = temperature;
     p.K = top_k;
     p.P = top_p;
@@ -2201,10 +1628,6 @@ int mxs_sample(const void* logits, int dtype, int B, int V, int64_t ld,
     p.out_tok = out_tokens;
     p.out_status = out_status;
     p.out_probs = out_probs;
-    char* ws = (char*)workspace;
-    p.parts = (ChunkOut*)(ws + L.parts);
-    p.cand_sk = (uint32_t*)(ws + L.cand_sk);
-    p.cand_idx = (uint32_t*)(ws + L.cand_idx);
 
     hipStream_t s = (hipStream_t)stream;
     hipError_t e = dtype == MXS_DTYPE_F32 ? launch<float>(p, s) : launch<__half>(p, s);

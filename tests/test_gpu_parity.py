@@ -244,3 +244,21 @@ def test_parity_one_workgroup_per_row_fallbacks(oracle, cuda):
     ref = run_oracle(oracle, w, probs=False)
     tok, st, _ = run_gpu(w, cuda, probs=False)
     check(w, ref, tok, st, None)
+
+
+@pytest.mark.parametrize("V", [1, 2, 7, 33, 1000])
+def test_parity_tiny_vocabularies(oracle, cuda, V):
+    """Rows shorter than one tile (element-by-element loads only), in every
+    row mode."""
+    rng = np.random.default_rng(V)
+    rows, params = [], []
+    for T, k, p, pen in [(0.0, 0, 1.0, 1.0), (0.0, 0, 1.0, 1.5), (0.8, 0, 0.9, 1.2), (0.8, 1, 1.0, 1.0),
+                         (1.1, 3, 0.7, 1.0), (0.9, V, 0.5, 0.8), (-0.5, 2, 0.9, 1.3), (0.7, 0, 1e-7, 1.0)]:
+        rows.append(rng.standard_normal(V).astype(np.float32))
+        params.append((T, k, p, pen, [0, V - 1, 0], float(rng.random())))
+    T, k, p, pen, h, u = (list(c) for c in zip(*params))
+    w = custom("tiny", np.stack(rows), T, k, p, pen, h, u)
+    say(f"[tiny] V={V} rows={w.B}")
+    ref = run_oracle(oracle, w)
+    tok, st, probs = run_gpu(w, cuda)
+    check(w, ref, tok, st, probs)
