@@ -127,14 +127,98 @@ __host__ __device__ __forceinline__ float clamp_uniform(float u)
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
 
+// ---------------------------------------------------------------- DPP wave operations
+//
+// Wave-wide prefix operations through DPP lane moves, which stay in the
+// vector ALU (no LDS round trips): shifts by 1, 2, 4 and 8 within each row of
+// 16 lanes, then row 0's result into row 1 and row 2's into row 3
+// (row_bcast:15), then lane 31's into rows 2 and 3 (row_bcast:31).  Lanes
+// without a source receive the operation's identity.  Every lane of the wave
+// must be active.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t dpp_move_or(uint32_t v, uint32_t id)
+{
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)id, (int)v, CTRL, ROWS, 0xF, false);
+}
+template <int CTRL, int ROWS>
+__device__ __forceinline__ u64 dpp_move64_or(u64 v, u64 id)
+{
+    const uint32_t lo = dpp_move_or<CTRL, ROWS>((uint32_t)v, (uint32_t)id);
+    const uint32_t hi = dpp_move_or<CTRL, ROWS>((uint32_t)(v >> 32), (uint32_t)(id >> 32));
+    return ((u64)hi << 32) | lo;
+}
+__device__ __forceinline__ uint32_t dpp_step(uint32_t v, uint32_t id, int step)
+{
+    switch (step) {
+    case 0: return dpp_move_or<0x111, 0xF>(v, id);
+    case 1: return dpp_move_or<0x112, 0xF>(v, id);
+    case 2: return dpp_move_or<0x114, 0xF>(v, id);
+    case 3: return dpp_move_or<0x118, 0xF>(v, id);
+    case 4: return dpp_move_or<0x142, 0xA>(v, id);
+    default: return dpp_move_or<0x143, 0xC>(v, id);
+    }
+}
+__device__ __forceinline__ u64 dpp_step(u64 v, u64 id, int step)
+{
+    switch (step) {
+    case 0: return dpp_move64_or<0x111, 0xF>(v, id);
+    case 1: return dpp_move64_or<0x112, 0xF>(v, id);
+    case 2: return dpp_move64_or<0x114, 0xF>(v, id);
+    case 3: return dpp_move64_or<0x118, 0xF>(v, id);
+    case 4: return dpp_move64_or<0x142, 0xA>(v, id);
+    default: return dpp_move64_or<0x143, 0xC>(v, id);
+    }
+}
+// Inclusive prefix of op over the wave (32- or 64-bit unsigned values).
+template <typename T, class Op>
+__device__ __forceinline__ T wave_prefix_op(T v, T id, Op op)
+{
+#pragma unroll
+    for (int step = 0; step < 6; ++step) v = op(v, dpp_step(v, id, step));
+    return v;
+}
+template <typename T>
+__device__ __forceinline__ T lane63(T v)
+{
+    if constexpr (sizeof(T) == 8) {
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 63);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((u64)v >> 32), 63);
+        return (T)(((u64)hi << 32) | lo);
+    } else {
+        return (T)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 63);
+    }
+}
+// Wave-wide results, in every lane.
+template <typename T> __device__ __forceinline__ T wave_max(T v)
+{
+    return lane63(wave_prefix_op<T>(v, (T)0, [](T a, T b) { return a > b ? a : b; }));
+}
+template <typename T> __device__ __forceinline__ T wave_sum(T v)
+{
+    return lane63(wave_prefix_op<T>(v, (T)0, [](T a, T b) { return a + b; }));
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) { return wave_max<uint32_t>(v); }
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) { return wave_sum<uint32_t>(v); }
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v)
+{
+    return lane63(wave_prefix_op<uint32_t>(v, 0xFFFFFFFFu, [](uint32_t a, uint32_t b) { return a < b ? a : b; }));
+}
+__device__ __forceinline__ uint32_t wave_or_u32(uint32_t v)
+{
+    return lane63(wave_prefix_op<uint32_t>(v, 0u, [](uint32_t a, uint32_t b) { return a | b; }));
+}
+__device__ __forceinline__ u64 wave_prefix_u64(u64 v)
+{
+    return wave_prefix_op<u64>(v, 0ull, [](u64 a, u64 b) { return a + b; });
+}
+
+// ---------------------------------------------------------------- block operations
+
 template <typename T>
 __device__ __forceinline__ T block_max(T v)
 {
     __shared__ T s[NWAVES];
-    for (int o = 32; o > 0; o >>= 1) {
-        T w = __shfl_xor(v, o, 64);
-        v = w > v ? w : v;
-    }
+    v = wave_max<T>(v);
     __syncthreads();
     if (lane_id() == 0) s[wave_id()] = v;
     __syncthreads();
@@ -155,7 +239,7 @@ template <typename T>
 __device__ __forceinline__ T block_sum(T v)
 {
     __shared__ T s[NWAVES];
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    v = wave_sum<T>(v);
     __syncthreads();
     if (lane_id() == 0) s[wave_id()] = v;
     __syncthreads();
@@ -170,13 +254,10 @@ template <typename T>
 __device__ __forceinline__ T block_incl_scan(T v, T* total)
 {
     __shared__ T s[NWAVES];
-    const int lane = lane_id(), w = wave_id();
-    for (int o = 1; o < 64; o <<= 1) {
-        T y = __shfl_up(v, o, 64);
-        if (lane >= o) v += y;
-    }
+    const int w = wave_id();
+    v = wave_prefix_op<T>(v, (T)0, [](T a, T b) { return a + b; });
     __syncthreads();
-    if (lane == 63) s[w] = v;
+    if (lane_id() == 63) s[w] = v;
     __syncthreads();
     T off = 0, tot = 0;
 #pragma unroll

@@ -49,30 +49,21 @@ __device__ __forceinline__ RowMode classify(float T, int k, int V)
     return MODE_LARGE;
 }
 
+// 16-byte vectors of a row (clang vector types, which load from any
+// address space) and the conversion of their elements to float.
 template <typename TIn> struct VecIO;
 template <> struct VecIO<float> {
     static constexpr int W = 4;
-    typedef float4 vec_t;
-    __device__ static void put(float* dst, const vec_t& v) { *(float4*)dst = v; }
+    typedef float vec_t __attribute__((ext_vector_type(4)));
     __device__ static void unpack(const vec_t& v, float* d) { d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w; }
     __device__ static float one(const float* p, int i) { return p[i]; }
 };
 template <> struct VecIO<__half> {
     static constexpr int W = 8;
-    typedef uint4 vec_t;
+    typedef uint32_t vec_t __attribute__((ext_vector_type(4)));
     __device__ static float h2f(uint32_t bits16)
     {
         return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
-    }
-    __device__ static void put(float* dst, const vec_t& v)
-    {
-        float4 a, b;
-        a.x = h2f(v.x & 0xFFFFu); a.y = h2f(v.x >> 16);
-        a.z = h2f(v.y & 0xFFFFu); a.w = h2f(v.y >> 16);
-        b.x = h2f(v.z & 0xFFFFu); b.y = h2f(v.z >> 16);
-        b.z = h2f(v.w & 0xFFFFu); b.w = h2f(v.w >> 16);
-        *(float4*)dst = a;
-        *(float4*)(dst + 4) = b;
     }
     __device__ static void unpack(const vec_t& v, float* d)
     {
@@ -134,12 +125,9 @@ struct Reduced {
 __device__ __forceinline__ Reduced block_reduce(uint32_t a, uint32_t b, uint32_t c)
 {
     __shared__ uint32_t s[3][NWAVES];
-    for (int o = 32; o > 0; o >>= 1) {
-        const uint32_t a2 = __shfl_xor(a, o, 64), b2 = __shfl_xor(b, o, 64), c2 = __shfl_xor(c, o, 64);
-        a = a2 > a ? a2 : a;
-        b = b2 < b ? b2 : b;
-        c |= c2;
-    }
+    a = wave_max_u32(a);
+    b = wave_min_u32(b);
+    c = wave_or_u32(c);
     __syncthreads();
     if (lane_id() == 0) { s[0][wave_id()] = a; s[1][wave_id()] = b; s[2][wave_id()] = c; }
     __syncthreads();
@@ -695,6 +683,288 @@ __device__ __forceinline__ bool finish_kept(const Params& p, int r, u64* keys, u
     return true;
 }
 
+// ---------------------------------------------------------------- top-k from the stream's segments
+//
+// The common top-k case, finished from the stream's per-wave buffer segments
+// as they are (no compaction).  The buffer holds every element whose
+// tempered value l reaches l_est = l(est), and the k-th largest l is at least
+// l_est.  One pass histograms the counts and masses of those elements over
+// 2048 bins linear in d = l - m on [l_est - m, 0] (monotone in the sorted
+// order).  Then one wave finds the bin of the k-th largest, of the top-p cut
+// and of the draw; each of these is resolved by gathering that bin's elements
+// (at most 64) and ranking them within the wave.  The other waves only help
+// to gather.
+
+__device__ __forceinline__ u64 readlane64(u64 v, int l)
+{
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l);
+    return ((u64)hi << 32) | lo;
+}
+
+// Inclusive sums over the wave's lanes: from lane 0 up (prefix), from lane 63
+// down (suffix); the wave's total.
+__device__ __forceinline__ u64 wave_prefix_incl(u64 v) { return wave_prefix_u64(v); }
+__device__ __forceinline__ u64 wave_sum64(u64 v) { return readlane64(wave_prefix_u64(v), 63); }
+__device__ __forceinline__ u64 wave_suffix_incl(u64 v)
+{
+    const u64 pre = wave_prefix_u64(v);
+    return readlane64(pre, 63) - pre + v;
+}
+
+struct WHit {
+    int bin;
+    u64 above;   // sum of the bins above `bin`
+};
+
+// Called by one whole wave, lane L holding s = the sum of h[32L, 32L + 32):
+// the bin b of h[0, 2048) with above(b) <= t < above(b) + h[b], where
+// above(b) is the sum of the bins above b.  Requires t < the total.
+template <typename T>
+__device__ __forceinline__ WHit wave_find_desc(const T* h, u64 s, u64 t)
+{
+    const int lane = lane_id();
+    const u64 incl = wave_suffix_incl(s);
+    const u64 msk = __ballot(incl - s <= t && t < incl);
+    const int L = msk ? __builtin_ctzll(msk) : 0;
+    const u64 a = readlane64(incl - s, L);
+    // lane L's 32 bins, highest first, one per lane
+    const u64 v = lane < 32 ? (u64)h[32 * L + 31 - lane] : 0ull;
+    const u64 pi = wave_prefix_incl(v);
+    const u64 m2 = __ballot(lane < 32 && a + pi - v <= t && t < a + pi);
+    const int j = m2 ? __builtin_ctzll(m2) : 0;
+    return WHit{32 * L + 31 - j, a + readlane64(pi - v, j)};
+}
+
+// Called by one whole wave: the sum of h over the bins above b.
+template <typename T>
+__device__ __forceinline__ u64 wave_sum_above(const T* h, u64 s, int b)
+{
+    const int lane = lane_id();
+    const int L = b >> 5, i = b & 31;
+    u64 v = lane > L ? s : 0ull;
+    if (lane < 32 && lane > i) v += (u64)h[32 * L + lane];
+    return wave_sum64(v);
+}
+
+// Ranks of a gathered bin (n <= 64 keys in LDS, any order), one element per
+// lane: its key, mass, the number of keys above it and their mass.
+struct Ranked {
+    u64 key, w, E;
+    uint32_t gt;
+    bool valid;
+};
+__device__ __forceinline__ Ranked rank_gathered(const u64* keys, const u64* ws, uint32_t n)
+{
+    const uint32_t lane = (uint32_t)lane_id();
+    Ranked q{0ull, 0ull, 0ull, 0u, lane < n};
+    if (q.valid) { q.key = keys[lane]; q.w = ws[lane]; }
+    for (uint32_t i = 0; i < n; ++i) {   // broadcast reads of the gathered keys
+        const u64 o = keys[i];
+        const bool above = o > q.key;
+        q.gt += above ? 1u : 0u;
+        q.E += above ? ws[i] : 0ull;
+    }
+    return q;
+}
+
+// Input, from the kernel's pass over the segments: every buffered element
+// with l >= l_est carries its bin + 1 in bits 18 and up of its id word
+// (V <= 2^18), the others 0 there; CH / MH hold the counts and masses
+// mass_of(l - m) per bin, CS / MS per group of 32 bins.  Returns false,
+// having written nothing, when a bin holds more than 64 elements: the
+// caller then takes the general path.
+constexpr int TAG_SHIFT = 18;
+constexpr uint32_t ID_MASK = (1u << TAG_SHIFT) - 1u;
+static_assert(MXS_MAX_VOCAB <= (1 << TAG_SHIFT), "ids and bin tags share a word");
+
+__device__ __forceinline__ bool finish_segs(const Params& p, int r, const uint32_t* ck, const uint32_t* ci,
+                                            const uint32_t* seg, float T, bool neg, uint32_t kk, float m,
+                                            float top_p, float u, const u64* MH, const uint32_t* CH,
+                                            const u64* MS, const uint32_t* CS, int64_t& tok, int32_t& st)
+{
+    __shared__ u64 g_key[2][64], g_w[2][64];
+    __shared__ uint32_t g_n[2];
+    __shared__ int g_req[2];     // bins to gather next (-1: none)
+    __shared__ int g_fail;
+    __shared__ u64 g_tok, g_wk, g_cut;
+    __shared__ uint32_t g_vkk;
+    __shared__ int g_st, g_bounded;
+    const int wv = wave_id(), lane = lane_id();
+    const uint32_t cw = seg[wv];
+    const uint32_t* wck = ck + wv * FSEG;
+    const uint32_t* wci = ci + wv * FSEG;
+
+    // Wave 0 resolves the row in phases; each phase names the bins that the
+    // workgroup gathers for the next one.
+    enum { PH_K, PH_CUT, PH_DRAW, PH_DONE };
+    int phase = PH_K;
+    u64 cs = 0, ms = 0;      // this lane's group of 32 bins
+    u64 Ak = 0, W = 0, Wk = 0, t = 0, D = 0, Ac = 0, Ad = 0, cutkey = 0, nabove = 0;
+    uint32_t vkk = 0;
+    int kb = 0, bd = -1;
+    bool bounded = false;
+    int32_t rst = MXS_ROW_OK;
+    u64 dkey = 0;
+    if (threadIdx.x == 0) { g_n[0] = 0; g_n[1] = 0; g_req[1] = -1; g_fail = 0; }
+    if (wv == 0) {
+        cs = CS[lane];
+        ms = MS[lane];
+        const WHit hk = wave_find_desc<uint32_t>(CH, cs, (u64)(kk - 1u));
+        kb = hk.bin;
+        nabove = hk.above;
+        Ak = wave_sum_above<u64>(MH, ms, kb);
+        if (lane == 0) g_req[0] = kb;
+    }
+    for (int round = 0;; ++round) {   // (wave 0 is done, or has failed, within three rounds)
+        __syncthreads();
+        const int rq0 = g_req[0], rq1 = g_req[1];
+        if (g_fail) return false;
+        if (rq0 < 0 && rq1 < 0) break;
+        const uint32_t tg0 = (uint32_t)(rq0 + 1), tg1 = (uint32_t)(rq1 + 1);
+        for (uint32_t j = (uint32_t)lane; j < cw; j += 64) {   // gather the requested bins
+            const uint32_t word = wci[j];
+            const uint32_t tag = word >> TAG_SHIFT;
+            if (tag != 0u && (tag == tg0 || tag == tg1)) {
+                const float l = sel_inv(wck[j], neg) / T;
+                const int li = tag == tg0 ? 0 : 1;
+                const uint32_t slot = atomicAdd(&g_n[li], 1u);
+                if (slot < 64u) {
+                    g_key[li][slot] = ((u64)vkey(l) << 32) | (u64)(0xFFFFFFFFu - (word & ID_MASK));
+                    g_w[li][slot] = mass_of(l - m);
+                }
+            }
+        }
+        __syncthreads();
+        const uint32_t n0 = g_n[0], n1 = g_n[1];
+        if (n0 > 64u || n1 > 64u) return false;
+        __syncthreads();   // (every wave has read the counts)
+        if (wv == 0) {
+            const Ranked q0 = rank_gathered(g_key[0], g_w[0], n0);
+            const Ranked q1 = rank_gathered(g_key[1], g_w[1], n1);
+            int next0 = -1, next1 = -1;
+            bool fail = false;
+            // the key, mass and mass before it of the element of list q whose
+            // mass interval, offset by A, holds x
+            auto pick = [&](const Ranked& q, bool elig, u64 A, u64 x, u64& key, u64& E, u64& w) {
+                const u64 mk = __ballot(elig && A + q.E <= x && x < A + q.E + q.w);
+                if (!mk) { fail = true; return; }
+                const int l0 = __builtin_ctzll(mk);
+                key = readlane64(q.key, l0);
+                E = A + readlane64(q.E, l0);
+                w = readlane64(q.w, l0);
+            };
+            // the draw once Wk is known: from list q (offset A) or a bin above it
+            auto draw_from = [&](const Ranked& q, bool elig, u64 A) {
+                D = floor_mul(clamp_uniform(u), Wk);   // sampling.py:69
+                if (D >= A) {
+                    u64 E, w;
+                    pick(q, elig, A, D, dkey, E, w);
+                    phase = PH_DONE;
+                } else {
+                    const WHit hd = wave_find_desc<u64>(MH, ms, D);
+                    bd = hd.bin;
+                    Ad = hd.above;
+                    next0 = bd;
+                    phase = PH_DRAW;
+                }
+            };
+            if (phase == PH_K) {
+                // sampling.py:52-54: the k-th largest of the bin; its value ties stay
+                const uint32_t rk = (kk - 1u) - (uint32_t)nabove;
+                const u64 mk = __ballot(q0.valid && q0.gt == rk);
+                if (!mk) fail = true;
+                vkk = (uint32_t)(readlane64(q0.key, mk ? __builtin_ctzll(mk) : 0) >> 32);
+                const bool kept = q0.valid && (uint32_t)(q0.key >> 32) >= vkk;
+                W = Ak + wave_sum64(kept ? q0.w : 0ull);
+                Wk = W;
+                if (top_p < 1.0f && !(top_p > 0.0f)) {
+                    rst = MXS_ROW_EMPTY_NUCLEUS;
+                    phase = PH_DONE;
+                } else if (top_p < 1.0f) {   // sampling.py:56-63
+                    t = ceil_mul(top_p, W) - 1;
+                    bounded = true;
+                    if (t >= Ak) {
+                        u64 E, w;
+                        pick(q0, kept, Ak, t, cutkey, E, w);
+                        Wk = E + w;
+                        draw_from(q0, kept, Ak);
+                    } else {
+                        const WHit hc = wave_find_desc<u64>(MH, ms, t);
+                        Ac = hc.above;
+                        next0 = hc.bin;
+                        phase = PH_CUT;
+                        // Wk will lie in (Ac, Ac + MH[cut's bin]]: when the draw
+                        // position lands in one bin above the cut's bin at both
+                        // ends, gather that bin now as well
+                        const float uc = clamp_uniform(u);
+                        const u64 Dlo = floor_mul(uc, Ac + 1), Dhi = floor_mul(uc, Ac + MH[hc.bin]);
+                        if (Dhi < Ac) {
+                            const WHit h1 = wave_find_desc<u64>(MH, ms, Dlo);
+                            const WHit h2 = wave_find_desc<u64>(MH, ms, Dhi);
+                            if (h1.bin == h2.bin) { bd = h1.bin; Ad = h1.above; next1 = bd; }
+                        }
+                    }
+                } else {
+                    draw_from(q0, kept, Ak);
+                }
+            } else if (phase == PH_CUT) {   // the cut's bin lies wholly in the top-k set
+                u64 E, w;
+                pick(q0, q0.valid, Ac, t, cutkey, E, w);
+                Wk = E + w;
+                D = floor_mul(clamp_uniform(u), Wk);
+                if (bd >= 0 && D < Ac) {   // the bin gathered alongside
+                    pick(q1, q1.valid, Ad, D, dkey, E, w);
+                    phase = PH_DONE;
+                } else {
+                    draw_from(q0, q0.valid, Ac);
+                }
+            } else if (phase == PH_DRAW) {
+                u64 E, w;
+                pick(q0, q0.valid, Ad, D, dkey, E, w);
+                phase = PH_DONE;
+            }
+            if (round >= 2 && phase != PH_DONE) fail = true;
+            if (lane == 0) {
+                g_n[0] = 0;
+                g_n[1] = 0;
+                g_req[0] = phase == PH_DONE ? -1 : next0;
+                g_req[1] = phase == PH_DONE ? -1 : next1;
+                if (fail) g_fail = 1;
+                if (phase == PH_DONE) {
+                    g_tok = dkey;
+                    g_wk = Wk;
+                    g_cut = cutkey;
+                    g_vkk = vkk;
+                    g_st = rst;
+                    g_bounded = bounded ? 1 : 0;
+                }
+            }
+        }
+    }
+    // (the loop ends at a barrier after wave 0's last phase)
+    st = g_st;
+    if (st != MXS_ROW_OK) { tok = -1; return true; }
+    tok = (int64_t)(0xFFFFFFFFu - (uint32_t)g_tok);
+    if (p.out_probs) {   // sampling.py:68
+        const u64 wkk = g_wk, cut = g_cut;
+        const uint32_t vk_k = g_vkk;
+        const bool bnd = g_bounded != 0;
+        float* out = p.out_probs + (size_t)r * (size_t)p.V;
+        for (uint32_t j = (uint32_t)lane; j < cw; j += 64) {
+            const uint32_t word = wci[j];
+            if (word >> TAG_SHIFT) {
+                const float l = sel_inv(wck[j], neg) / T;
+                const uint32_t id = word & ID_MASK;
+                const u64 key = ((u64)vkey(l) << 32) | (u64)(0xFFFFFFFFu - id);
+                if (bnd ? key >= cut : (uint32_t)(key >> 32) >= vk_k)
+                    out[id] = (float)((double)mass_of(l - m) / (double)wkk);
+            }
+        }
+    }
+    return true;
+}
+
 // ================================================================ k_fused
 //
 // One workgroup per row, the whole chain in one launch.  The row streams from
@@ -715,50 +985,79 @@ __device__ __forceinline__ bool finish_kept(const Params& p, int r, u64* keys, u
 // elem(i, e, x) for slot i in [0, 16) of this thread's share of the tile,
 // element index e and its penalized value x; then tile_end(id), called by all
 // threads (it may synchronize), where id(i) is the element index of slot i in
-// that tile; it returns true to stop the stream.  Slot i of a tile is skipped
-// when it lies past the row's end.
+// that tile; it returns true to stop the stream.  Slots past the row's end
+// are skipped; in every wave the lanes that skip a slot are its highest
+// ones, so a ballot taken in elem is complete in lane 0.
 //
-// Whole tiles are loaded with unconditional 128-bit loads, alternating two
-// register buffers so that the next tile is in flight while this one is
-// processed (conditional loads would make the compiler wait for all of them).
+// A row that starts on a 16-byte boundary is read in 128-bit loads, one tile
+// per register buffer, two buffers alternating so that the next tile is in
+// flight while this one is processed.  The loads are unconditional (vectors
+// past the row's end read its last vector again, tiles past the end its last
+// tile): a branch around loads makes the compiler wait for all of them.
+// Constructing a RowStream issues the first two tiles, so a kernel can create
+// it before its set-up and overlap the two; run() consumes it once, restart()
+// issues the first tiles again.
 constexpr int FPT = FTILE / NT;   // logits per thread per tile (16)
 
-// PEN: apply the penalty from the bitmap while streaming (a separate
-// instantiation, so that rows without it carry no branches in the loop: a
-// branch around loads or their uses makes the compiler wait for every load
-// in flight).
-template <typename TIn, bool PEN, class Elem, class TileEnd>
-__device__ __forceinline__ void stream_row(const TIn* rowp, int V, const uint32_t* bm, float pen,
-                                           Elem&& elem, TileEnd&& tile_end)
-{
-    typedef VecIO<TIn> IO;
-    constexpr int VW = IO::W;
-    constexpr int FU = FPT / VW;            // 16-byte loads per thread per tile
-    constexpr int TV = NT * FU;             // vectors per tile
-    typedef typename IO::vec_t vec_t;
-    const int tid = threadIdx.x;
-    const bool vec_ok = (((uintptr_t)rowp) & 15u) == 0;
-    const int nfull = vec_ok ? V / (TV * VW) : 0;   // tiles wholly inside the row
-    const vec_t* src = (const vec_t*)rowp;
+__device__ __align__(16) const uint4 g_zero_vec = {0u, 0u, 0u, 0u};
 
-    auto load = [&](vec_t (&b)[FU], int t) {
+template <typename TIn>
+struct RowStream {
+    typedef VecIO<TIn> IO;
+    static constexpr int VW = IO::W;
+    static constexpr int FU = FPT / VW;   // 16-byte loads per thread per tile
+    static constexpr int TV = NT * FU;    // vectors per tile
+    typedef typename IO::vec_t vec_t;
+
+    const TIn* rowp;
+    int V, nvec, ntile;
+    vec_t A[FU], Bf[FU];
+
+    __device__ __forceinline__ RowStream(const TIn* rp, int v) : rowp(rp), V(v)
+    {
+        nvec = ((((uintptr_t)rp) & 15u) == 0) ? v / VW : 0;
+        ntile = (nvec + TV - 1) / TV;
+        restart();
+    }
+    __device__ __forceinline__ void restart()
+    {
+        load(A, 0);
+        load(Bf, 1);
+    }
+    // (no branch: a row with no whole vector reads a dummy vector instead)
+    __device__ __forceinline__ void load(vec_t (&b)[FU], int t)
+    {
+        typedef const __attribute__((address_space(1))) vec_t* gptr;   // global memory: plain vector loads
+        const gptr src = nvec > 0 ? (gptr)rowp : (gptr)&g_zero_vec;
+        const int lastv = nvec > 0 ? nvec - 1 : 0;
+        t = t < ntile ? t : ntile - 1;
+        t = t > 0 ? t : 0;
 #pragma unroll
-        for (int j = 0; j < FU; ++j) b[j] = src[t * TV + j * NT + tid];
-    };
-    auto proc = [&](const vec_t (&b)[FU], int t) {
+        for (int j = 0; j < FU; ++j) {
+            const int vi = t * TV + j * NT + (int)threadIdx.x;
+            b[j] = src[vi < lastv ? vi : lastv];
+        }
+    }
+    // PART: the last tile, which may end inside the row's vectors
+    template <bool PART, bool PEN, class Elem>
+    __device__ __forceinline__ void proc(const vec_t (&b)[FU], int t, const uint32_t* bm, float pen, Elem& elem)
+    {
+        const int tid = threadIdx.x;
         uint32_t hw[FU];   // the history bitmap words of this tile, read together
         if constexpr (PEN) {
 #pragma unroll
             for (int j = 0; j < FU; ++j) {
-                const int e = (t * TV + j * NT + tid) * VW;
-                hw[j] = bm[e >> 5];
+                const int vi = t * TV + j * NT + tid;
+                hw[j] = (!PART || vi < nvec) ? bm[(vi * VW) >> 5] : 0u;
             }
         }
 #pragma unroll
         for (int j = 0; j < FU; ++j) {
+            const int vi = t * TV + j * NT + tid;
+            if (PART && vi >= nvec) continue;
             float xs[VW];
             IO::unpack(b[j], xs);
-            const int e = (t * TV + j * NT + tid) * VW;
+            const int e = vi * VW;
             if constexpr (PEN) {
                 const uint32_t bits = (hw[j] >> (e & 31)) & ((1u << VW) - 1u);
                 if (bits) {
@@ -770,59 +1069,83 @@ __device__ __forceinline__ void stream_row(const TIn* rowp, int V, const uint32_
 #pragma unroll
             for (int q = 0; q < VW; ++q) elem(j * VW + q, e + q, xs[q]);
         }
-    };
-
-    // two tiles in flight: A holds tile t, B tile t + 1; indices past the
-    // last whole tile load that tile again (cached, never processed)
-    vec_t A[FU], Bf[FU];
-    const int last = nfull - 1;
-    if (nfull > 0) {
-        load(A, 0);
-        load(Bf, 1 < nfull ? 1 : last);
     }
-    auto vid = [&](int t) {
-        return [=](int i) { return (t * TV + (i / VW) * NT + tid) * VW + i % VW; };
-    };
-    for (int t = 0; t < nfull; t += 2) {
-        proc(A, t);
-        if (tile_end(vid(t))) return;
-        load(A, t + 2 < nfull ? t + 2 : last);
-        if (t + 1 < nfull) {
-            proc(Bf, t + 1);
+    template <bool PEN, class Elem, class TileEnd>
+    __device__ __forceinline__ void run(const uint32_t* bm, float pen, Elem&& elem, TileEnd&& tile_end)
+    {
+        const int tid = threadIdx.x;
+        const int nfull = nvec / TV;   // tiles wholly inside the row's vectors
+        auto vid = [&](int t) {
+            return [=](int i) { return (t * TV + (i / VW) * NT + tid) * VW + i % VW; };
+        };
+        // A holds tile t, Bf tile t + 1
+        int t = 0;
+        for (; t + 1 < nfull; t += 2) {
+            proc<false, PEN>(A, t, bm, pen, elem);
+            if (tile_end(vid(t))) return;
+            load(A, t + 2);
+            proc<false, PEN>(Bf, t + 1, bm, pen, elem);
             if (tile_end(vid(t + 1))) return;
+            load(Bf, t + 3);
         }
-        load(Bf, t + 3 < nfull ? t + 3 : last);
-    }
-    // the rest of the row (all of a row that is not 16-byte aligned), element by element
-    for (int e0 = nfull * FTILE; e0 < V; e0 += FTILE) {
-        float xs[FPT];
+        if (t < nfull) {
+            proc<false, PEN>(A, t, bm, pen, elem);
+            if (tile_end(vid(t))) return;
+            ++t;
 #pragma unroll
-        for (int i = 0; i < FPT; ++i) {
-            const int e = e0 + i * NT + tid;
-            xs[i] = e < V ? IO::one(rowp, e) : 0.0f;
+            for (int j = 0; j < FU; ++j) A[j] = Bf[j];   // (one call site for the last tile)
         }
+        if (t < ntile) {
+            proc<true, PEN>(A, t, bm, pen, elem);
+            if (tile_end(vid(t))) return;
+        }
+        // the rest of the row (all of a row that is not 16-byte aligned), element by element
+        for (int e0 = nvec * VW; e0 < V; e0 += FTILE) {
+            float xs[FPT];
 #pragma unroll
-        for (int i = 0; i < FPT; ++i) {
-            const int e = e0 + i * NT + tid;
-            if (e < V) {
-                float x = xs[i];
-                if constexpr (PEN) {
-                    if ((bm[e >> 5] >> (e & 31)) & 1u) x = penalize(x, pen);
-                }
-                elem(i, e, x);
+            for (int i = 0; i < FPT; ++i) {
+                const int e = e0 + i * NT + tid;
+                xs[i] = e < V ? IO::one(rowp, e) : 0.0f;
             }
+#pragma unroll
+            for (int i = 0; i < FPT; ++i) {
+                const int e = e0 + i * NT + tid;
+                if (e < V) {
+                    float x = xs[i];
+                    if constexpr (PEN) {
+                        if ((bm[e >> 5] >> (e & 31)) & 1u) x = penalize(x, pen);
+                    }
+                    elem(i, e, x);
+                }
+            }
+            if (tile_end([=](int i) { return e0 + i * NT + tid; })) return;
         }
-        if (tile_end([=](int i) { return e0 + i * NT + tid; })) return;
     }
+    // run() with the inline penalty chosen at run time
+    template <class Elem, class TileEnd>
+    __device__ __forceinline__ void run_pen(const uint32_t* bm, bool pen_inline, float pen, Elem&& elem,
+                                            TileEnd&& tile_end)
+    {
+        if (pen_inline) run<true>(bm, pen, elem, tile_end);
+        else run<false>(bm, pen, elem, tile_end);
+    }
+};
+
+// One pass over a row from its first tile.
+template <typename TIn, bool PEN, class Elem, class TileEnd>
+__device__ __forceinline__ void stream_row(const TIn* rowp, int V, const uint32_t* bm, float pen,
+                                           Elem&& elem, TileEnd&& tile_end)
+{
+    RowStream<TIn> rs(rowp, V);
+    rs.template run<PEN>(bm, pen, elem, tile_end);
 }
 
-// stream_row with the inline penalty chosen at run time.
 template <typename TIn, class Elem, class TileEnd>
 __device__ __forceinline__ void stream_row_pen(const TIn* rowp, int V, const uint32_t* bm, bool pen_inline, float pen,
                                                Elem&& elem, TileEnd&& tile_end)
 {
-    if (pen_inline) stream_row<TIn, true>(rowp, V, bm, pen, elem, tile_end);
-    else stream_row<TIn, false>(rowp, V, bm, pen, elem, tile_end);
+    RowStream<TIn> rs(rowp, V);
+    rs.run_pen(bm, pen_inline, pen, elem, tile_end);
 }
 
 // Exclusive prefix over the wave of c (0 <= c < 32) and the wave's total,
@@ -1171,36 +1494,65 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
     __shared__ uint32_t s_seg[NWAVES];          // entries per buffer segment
     __shared__ uint32_t s_ovf;                  // a segment ran full
     __shared__ uint32_t s_nh;                   // distinct history ids listed in hl
-    __shared__ uint32_t s_reach[NWAVES];        // keys reaching the estimate, per segment
 
     const int tid = threadIdx.x, lane = lane_id();
     const int r = blockIdx.x;
     const int V = p.V;
-    const float T = p.T[r];
-    const int k = p.K[r];
-    const float pen = p.PEN[r];
+    const TIn* rowp = (const TIn*)p.logits + (size_t)r * (size_t)p.ld;
+    // Loads are issued in the order they are needed: the row's parameters,
+    // the sample for a top-k row's first bound, then the row's first two
+    // tiles (every valid row streams from its start, and the set-up below
+    // overlaps them).  Requests are served in issue order, so the tiles, the
+    // bulk, go last.
+    //
+    // The parameters: one gathered load, lane i of every wave reading
+    // parameter i (an absent optional array reads a valid dummy instead);
+    // they are read out of the lanes once the other loads are in flight.
+    const uint32_t* pa = (const uint32_t*)(p.T + r);
+    pa = lane == 1 ? (const uint32_t*)(p.K + r) : pa;
+    pa = lane == 2 ? (const uint32_t*)(p.PEN + r) : pa;
+    pa = lane == 3 ? (const uint32_t*)(p.P + r) : pa;
+    pa = (lane == 4 && p.hoff) ? (const uint32_t*)(p.hoff + r) : pa;
+    pa = (lane == 5 && p.hoff) ? (const uint32_t*)(p.hoff + r + 1) : pa;
+    pa = (lane == 6 && p.U) ? (const uint32_t*)(p.U + r) : pa;
+    const uint32_t pv = *pa;
+    // The sample: NSAMP logits in 64 groups of 32 consecutive ones spread
+    // over the row (a group is one 128-byte line of an fp32 row), 4 per
+    // thread.  It is requested before the row's mode is known, so that it
+    // does not queue behind the tiles; rows that do not use it waste 8 KB.
+    constexpr int NS = NSAMP / NT;
+    static_assert(NSAMP == 64 * 32 && NS * 8 == 32, "sample layout");
+    float sx[NS];
+    const int se0 = (((tid >> 3) * (V >> 6)) & ~31) + (tid & 7) * NS;   // this thread's first sample
+#pragma unroll
+    for (int q = 0; q < NS; ++q) sx[q] = VecIO<TIn>::one(rowp, se0 + q < V ? se0 + q : V - 1);
+    RowStream<TIn> rs(rowp, V);
+    __builtin_amdgcn_sched_barrier(0);   // (the loads above stay ahead of the reads below)
+    const float T = __builtin_bit_cast(float, (uint32_t)__builtin_amdgcn_readlane((int)pv, 0));
+    const int k = __builtin_amdgcn_readlane((int)pv, 1);
+    const float pen = __builtin_bit_cast(float, (uint32_t)__builtin_amdgcn_readlane((int)pv, 2));
+    const float top_p = __builtin_bit_cast(float, (uint32_t)__builtin_amdgcn_readlane((int)pv, 3));
+    const int hv0 = __builtin_amdgcn_readlane((int)pv, 4);
+    const int hv1 = __builtin_amdgcn_readlane((int)pv, 5);
+    const float uv = __builtin_bit_cast(float, (uint32_t)__builtin_amdgcn_readlane((int)pv, 6));
+    const int h0 = p.hoff ? hv0 : 0;
+    const int h1 = p.hoff ? hv1 : 0;
+    const float u = p.U ? uv : 0.0f;
     RowMode mode = classify(T, k, V);
     const bool neg = T < 0.0f;
-    const TIn* rowp = (const TIn*)p.logits + (size_t)r * (size_t)p.ld;
-    const int h0 = p.hoff ? p.hoff[r] : 0;
-    const int h1 = p.hoff ? p.hoff[r + 1] : 0;
     const bool pen_on = (pen != 1.0f) && (h1 > h0);
-    const float top_p = p.P[r];
-    const float u = p.U ? p.U[r] : 0.0f;
     int64_t tok = -1;
     int32_t st = MXS_ROW_OK;
 
-    // top-k rows: the strided sample for the first bound is requested first,
-    // so that its latency overlaps the set-up below
     const bool sampled = mode == MODE_TOPK && V >= FAST_MIN_V;
-    constexpr int NS = NSAMP / NT;
-    float sx[NS];
-    if (sampled) {
-        const int stride = V / NT;
-#pragma unroll
-        for (int q = 0; q < NS; ++q) sx[q] = VecIO<TIn>::one(rowp, tid * stride + q);
+    if (sampled)
         for (int b = tid; b < 2048; b += NT) hist[b] = 0;
-    }
+    // With 1 <= pen < inf and T > 0 the penalty never raises a selection
+    // key, so a top-k row's stream may compare raw keys: the raw hits include
+    // every penalized hit.  Buffered history ids get their penalized keys
+    // afterwards, and the history bitmap is first needed after the stream.
+    const bool defer = pen_on && !neg && pen >= 1.0f && pen <= 3.402823466e38f;
+    const bool late_bm = sampled && defer;
     if (p.out_probs) {
         float* o = p.out_probs + (size_t)r * (size_t)V;
         for (int i = tid; i < V; i += NT) o[i] = 0.0f;
@@ -1209,33 +1561,53 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
     if (tid < 3) s_cnt[tid] = 0;
 
     // sampling.py:38-45: the row's history ids, each once (sorted(set())).
+    // The first HB per thread are requested now and held in registers.
     // Rows with top-k off also list them (the thread that sets an id's bit
     // appends it) for the passes that correct raw values to penalized ones.
-    bool bad = false;
+    constexpr int HB = 4;
+    int hv[HB];
     uint32_t* hl = (uint32_t*)(smem + KF_HL);
     if (tid == 0) s_nh = 0;
     if (pen_on) {
+#pragma unroll
+        for (int q = 0; q < HB; ++q) {
+            const int h = h0 + tid + q * NT;
+            hv[q] = h < h1 ? p.hids[h] : 0;
+        }
         const int words = (V + 31) >> 5;
         for (int w = tid; w < words; w += NT) bm[w] = 0;
-        __syncthreads();
-        const bool list = mode == MODE_LARGE;
-        for (int h = h0 + tid; h < h1; h += NT) {
-            const int id = p.hids[h];
-            if (id < 0 || id >= V) { bad = true; continue; }
-            const uint32_t bit = 1u << (id & 31);
-            const uint32_t old = atomicOr(&bm[id >> 5], bit);
-            if (list && !(old & bit)) {
-                const uint32_t slot = atomicAdd(&s_nh, 1u);
-                if (slot < (uint32_t)HCAP) hl[slot] = (uint32_t)id;
-            }
-        }
     }
-    if (block_max<uint32_t>(bad ? 1u : 0u)) st = MXS_ROW_BAD_HISTORY;   // (its barriers publish bm)
-    else if (mode == MODE_INVALID) st = MXS_ROW_BAD_PARAM;
+    // Sets the bits of the row's history (after a barrier that follows the
+    // clearing above); returns whether this thread saw an id outside [0, V).
+    auto build_bitmap = [&]() -> bool {
+        bool bad = false;
+        if (pen_on) {
+            const bool list = mode == MODE_LARGE;
+            auto add = [&](int id) {
+                if (id < 0 || id >= V) { bad = true; return; }
+                const uint32_t bit = 1u << (id & 31);
+                const uint32_t old = atomicOr(&bm[id >> 5], bit);
+                if (list && !(old & bit)) {
+                    const uint32_t slot = atomicAdd(&s_nh, 1u);
+                    if (slot < (uint32_t)HCAP) hl[slot] = (uint32_t)id;
+                }
+            };
+#pragma unroll
+            for (int q = 0; q < HB; ++q)
+                if (h0 + tid + q * NT < h1) add(hv[q]);
+            for (int h = h0 + tid + HB * NT; h < h1; h += NT) add(p.hids[h]);
+        }
+        return bad;
+    };
+    if (!late_bm) {
+        __syncthreads();
+        if (block_max<uint32_t>(build_bitmap() ? 1u : 0u)) st = MXS_ROW_BAD_HISTORY;   // (its barriers publish bm)
+    }
+    if (st == MXS_ROW_OK && mode == MODE_INVALID) st = MXS_ROW_BAD_PARAM;
 
     if (st == MXS_ROW_OK && mode == MODE_GREEDY) {   // sampling.py:47-48
         uint32_t bk = 0, bi = 0;
-        stream_row_pen<TIn>(rowp, V, bm, pen_on, pen,
+        rs.run_pen(bm, pen_on, pen,
             [&](int, int e, float x) {
                 const uint32_t g = (x != x) ? 0xFFFFFFFFu : vkey(x);   // NaN is the maximum
                 if (g > bk) { bk = g; bi = (uint32_t)e; }              // ascending e: the first maximum
@@ -1252,11 +1624,8 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
         int cidx = 0;
         bool overflow = false;
         const uint32_t kk = (uint32_t)k;
-        // With 1 <= pen < inf and T > 0 the penalty never raises a selection
-        // key, so the stream may compare raw keys: the raw hits include every
-        // penalized hit.  Buffered history ids get their penalized keys
-        // (fix_up) before any bound is taken from the buffer.
-        const bool defer = pen_on && !neg && pen >= 1.0f && pen <= 3.402823466e38f;
+        // deferred penalty: buffered history ids get their penalized keys
+        // (fix_up) before any bound is taken from the buffer
         uint32_t Nfix = 0;   // buffer entries [0, Nfix) hold penalized keys
         auto fix_up = [&]() {
             if (defer) {
@@ -1268,20 +1637,27 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
             }
             Nfix = Nc;
         };
+        uint32_t est = 0, cmax = 0;   // the sampled estimate; the buffer's largest penalized key
+        bool segs = false;            // the candidates are in the stream's per-wave segments
+        bool binned = false;          // ... and carry their bins, counts and final masses
+        float m0 = 0.0f, lest = 0.0f;
+        Reduced rd{0u, 0xFFFFFFFFu, 0u};
+        u64* MH = (u64*)(smem + KF_MH);
+        __shared__ u64 s_ms[64];
+        __shared__ uint32_t s_cs[64];
+        __shared__ uint32_t s_r[5][NWAVES];
         if (mode == MODE_TOPK) {
             // 1. A conservative estimate of the k-th largest key from a strided
             //    sample of NSAMP logits: the lower edge of the histogram bin
             //    holding the sample's j-th largest, j well above the expected
             //    k * NSAMP / V.  It only steers the stream; step 3 checks it.
             bool fast = sampled;
-            uint32_t est = 0;
             if (tid == 0) s_ovf = 0u;
             if (fast) {
-                const int stride = V / NT;
                 uint32_t sk4[NS], smax = 0, smin = 0xFFFFFFFFu;
 #pragma unroll
                 for (int q = 0; q < NS; ++q) {
-                    const int e = tid * stride + q;
+                    const int e = se0 + q;   // (< V: rows that sample are long)
                     float x = sx[q];
                     if (pen_on && !defer && ((bm[e >> 5] >> (e & 31)) & 1u)) x = penalize(x, pen);
                     sk4[q] = selkey(x, neg);
@@ -1314,7 +1690,7 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                 u64 wm[FPT];        // wave ballots of the hits, per slot
 #pragma unroll
                 for (int i = 0; i < FPT; ++i) wm[i] = 0;
-                stream_row_pen<TIn>(rowp, V, bm, pen_on && !defer, pen,
+                rs.run_pen(bm, pen_on && !defer, pen,
                     [&](int i, int, float x) {
                         const uint32_t sk = selkey(x, neg);
                         omax = sk > omax ? sk : omax;
@@ -1323,9 +1699,15 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                         wm[i] = __ballot(sk >= theta);
                     },
                     [&](auto&& id) -> bool {
+                        // the ballots as lane 0 holds them (a slot past the row's end
+                        // skips a wave's highest lanes)
                         uint32_t tot = 0;
 #pragma unroll
-                        for (int i = 0; i < FPT; ++i) tot += (uint32_t)__builtin_popcountll(wm[i]);
+                        for (int i = 0; i < FPT; ++i) {
+                            wm[i] = ((u64)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(wm[i] >> 32)) << 32) |
+                                    (u64)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)wm[i]);
+                            tot += (uint32_t)__builtin_popcountll(wm[i]);
+                        }
                         if (cw + tot > (uint32_t)FSEG) {
                             if (lane == 0) __hip_atomic_store(&s_ovf, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
                             return true;
@@ -1346,56 +1728,110 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                         return __hip_atomic_load(&s_ovf, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0u;
                     });
                 if (lane == 0) s_seg[w] = cw;
-                __syncthreads();
-                fast = s_ovf == 0u;
-                if (fast) {
-                    // 3. Each wave reads its own segment into registers,
-                    //    penalizes its history ids and counts the keys that
-                    //    reach the estimate; after a barrier it writes them
-                    //    packed at its offset, so the buffer becomes [0, Nc).
-                    //    The estimate stands if at least k keys reach it (then
-                    //    the k-th largest key is >= est, and every element that
-                    //    ties with it after x / T is >= widen(est) = theta).
-                    constexpr int PERW = FSEG / 64;
-                    uint32_t off = 0;
-                    Nc = 0;
+                bool bad = false;
+                if (late_bm) bad = build_bitmap();
+                for (int b = tid; b < 2048; b += NT) { MH[b] = 0; hist[b] = 0; }
+                if (tid < 64) { s_cs[tid] = 0; s_ms[tid] = 0; }
+                {
+                    const uint32_t a2 = wave_max_u32(omax), a3 = wave_min_u32(omin);
+                    if (lane == 0) { s_r[2][w] = a2; s_r[3][w] = a3; }
+                }
+                __syncthreads();   // (publishes bm, s_seg, the cleared histograms)
+                rd = Reduced{0u, 0xFFFFFFFFu, 0u};
 #pragma unroll
-                    for (int v = 0; v < NWAVES; ++v) {
-                        const uint32_t c = s_seg[v];
-                        off += v < w ? c : 0u;
-                        Nc += c;
+                for (int v = 0; v < NWAVES; ++v) {
+                    rd.max = s_r[2][v] > rd.max ? s_r[2][v] : rd.max;
+                    rd.min = s_r[3][v] < rd.min ? s_r[3][v] : rd.min;
+                }
+                // 3. One pass over each wave's own segment: the penalty of its
+                //    history ids (deferred penalty), the segment's largest key,
+                //    the keys that reach the estimate, and for every element
+                //    with l >= l_est = l(est) its bin (linear in d = l - m0 on
+                //    [l_est - m0, 0], m0 the tempered row maximum before the
+                //    deferred penalty), count and mass.  The estimate stands
+                //    if at least k keys reach it: then the k-th largest key is
+                //    >= est, and every element that ties with it after x / T
+                //    is >= widen(est) = theta, so it is in the buffer.  The
+                //    masses are final when the penalty left the maximum alone.
+                m0 = sel_inv(rd.max, neg) / T;
+                lest = sel_inv(est, neg) / T;
+                const float dlo = lest - m0;
+                const float scale = 2047.0f / -dlo;
+                binned = dlo < 0.0f && dlo > -INFINITY && __builtin_isfinite(scale) && __builtin_isfinite(m0);
+                uint32_t cmx = 0, nr = 0;
+                for (uint32_t j = (uint32_t)lane; j < cw; j += 64) {
+                    uint32_t key = wck[j];
+                    const uint32_t id = wci[j];
+                    if (defer && ((bm[id >> 5] >> (id & 31)) & 1u)) {
+                        key = okey(penalize(okey_inv(key), pen));
+                        wck[j] = key;
                     }
-                    uint32_t kv[PERW], iv[PERW], nr = 0;
-#pragma unroll
-                    for (int q = 0; q < PERW; ++q) {
-                        const uint32_t j = (uint32_t)(lane + 64 * q);
-                        kv[q] = 0u;
-                        iv[q] = 0u;
-                        if (j < cw) {
-                            kv[q] = wck[j];
-                            iv[q] = wci[j];
-                            if (defer && ((bm[iv[q] >> 5] >> (iv[q] & 31)) & 1u))
-                                kv[q] = okey(penalize(okey_inv(kv[q]), pen));
-                            nr += kv[q] >= est ? 1u : 0u;
+                    cmx = key > cmx ? key : cmx;
+                    nr += key >= est ? 1u : 0u;
+                    if (binned) {
+                        const float l = sel_inv(key, neg) / T;
+                        if (l >= lest) {
+                            const float d = l - m0;
+                            const float f = (d - dlo) * scale;
+                            const uint32_t b = f < 2047.0f ? (uint32_t)f : 2047u;
+                            const u64 wgt = mass_of(d);
+                            atomicAdd(&hist[b], 1u);
+                            atomicAdd(&MH[b], wgt);
+                            atomicAdd(&s_cs[b >> 5], 1u);
+                            atomicAdd(&s_ms[b >> 5], wgt);
+                            wci[j] = id | ((b + 1u) << TAG_SHIFT);
                         }
                     }
-                    uint32_t wr;
-                    (void)wave_excl_small(nr, wr);
-                    if (lane == 0) s_reach[w] = wr;
+                }
+                {
+                    const uint32_t a0 = wave_max_u32(cmx), a1 = wave_sum_u32(nr), a4 = wave_max_u32(bad ? 1u : 0u);
+                    if (lane == 0) { s_r[0][w] = a0; s_r[1][w] = a1; s_r[4][w] = a4; }
+                }
+                __syncthreads();
+                uint32_t reach = 0, badw = 0;
+                cmax = 0;
+                Nc = 0;
+#pragma unroll
+                for (int v = 0; v < NWAVES; ++v) {
+                    cmax = s_r[0][v] > cmax ? s_r[0][v] : cmax;
+                    reach += s_r[1][v];
+                    badw |= s_r[4][v];
+                    Nc += s_seg[v];
+                }
+                if (badw) st = MXS_ROW_BAD_HISTORY;
+                fast = st == MXS_ROW_OK && s_ovf == 0u && reach >= kk;
+                segs = fast;
+                if (segs && binned && cmax != rd.max) {
+                    // the penalty lowered the row's maximum: the bins and
+                    // masses again, relative to the penalized maximum
+                    m0 = sel_inv(cmax, neg) / T;
+                    const float dlo2 = lest - m0;
+                    const float scale2 = 2047.0f / -dlo2;
+                    binned = dlo2 < 0.0f && dlo2 > -INFINITY && __builtin_isfinite(scale2) && __builtin_isfinite(m0);
+                    for (int b = tid; b < 2048; b += NT) { MH[b] = 0; hist[b] = 0; }
+                    if (tid < 64) { s_cs[tid] = 0; s_ms[tid] = 0; }
                     __syncthreads();
-#pragma unroll
-                    for (int q = 0; q < PERW; ++q) {
-                        const uint32_t j = (uint32_t)(lane + 64 * q);
-                        if (j < cw) { ck[off + j] = kv[q]; ci[off + j] = iv[q]; }
+                    for (uint32_t j = (uint32_t)lane; j < cw; j += 64) {
+                        const uint32_t id = wci[j] & ID_MASK;
+                        uint32_t word = id;
+                        const float l = sel_inv(wck[j], neg) / T;
+                        if (binned && l >= lest) {
+                            const float d = l - m0;
+                            const float f = (d - dlo2) * scale2;
+                            const uint32_t b = f < 2047.0f ? (uint32_t)f : 2047u;
+                            const u64 wgt = mass_of(d);
+                            atomicAdd(&hist[b], 1u);
+                            atomicAdd(&MH[b], wgt);
+                            atomicAdd(&s_cs[b >> 5], 1u);
+                            atomicAdd(&s_ms[b >> 5], wgt);
+                            word = id | ((b + 1u) << TAG_SHIFT);
+                        }
+                        wci[j] = word;
                     }
-                    uint32_t reach = 0;
-#pragma unroll
-                    for (int v = 0; v < NWAVES; ++v) reach += s_reach[v];
-                    fast = reach >= kk;
                     __syncthreads();
                 }
             }
-            if (!fast) {
+            if (!fast && st == MXS_ROW_OK) {
                 // 4. The stream again with one shared buffer and a running
                 //    bound raised by compaction whenever it nears capacity.
                 theta = 0;
@@ -1405,7 +1841,8 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                 if (tid < 3) s_cnt[tid] = 0;
                 __syncthreads();
                 uint32_t tk[FPT], te[FPT], hm = 0;   // this tile's keys, ids and hits
-                stream_row_pen<TIn>(rowp, V, bm, pen_on && !defer, pen,
+                if (sampled) rs.restart();
+                rs.run_pen(bm, pen_on && !defer, pen,
                     [&](int i, int e, float x) {
                         const uint32_t sk = selkey(x, neg);
                         omax = sk > omax ? sk : omax;
@@ -1482,7 +1919,7 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                 if (!overflow) fix_up();
             }
         } else {
-            stream_row_pen<TIn>(rowp, V, bm, pen_on, pen,
+            rs.run_pen(bm, pen_on, pen,
                 [&](int, int, float x) {
                     const uint32_t sk = selkey(x, neg);
                     omax = sk > omax ? sk : omax;
@@ -1490,18 +1927,49 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                 },
                 [&](auto&&) { return false; });
         }
-        const Reduced rd = block_reduce(omax, omin, 0u);
+        if (!segs) rd = block_reduce(omax, omin, 0u);
         // NaN keys lie above the key of +inf and below that of -inf (the
         // reversed keys of T < 0 swap the two ranges)
         const bool has_nan = rd.max > 0xFF800000u || rd.min < 0x007FFFFFu;
         const bool has_inf = rd.max >= 0xFF800000u || rd.min <= 0x007FFFFFu;
-        if (has_nan || (has_inf && __builtin_isinf(T))) {
+        if (st != MXS_ROW_OK) {
+            // a history id outside [0, V), found after the stream
+        } else if (has_nan || (has_inf && __builtin_isinf(T))) {
             st = MXS_ROW_NONFINITE;   // a NaN tempered logit heads the order (sampling.py:57-58)
         } else {
             bool done = false;
             uint32_t thk = 0;
             bool thk_known = false;
-            if (mode == MODE_TOPK && !overflow) {
+            if (segs) {
+                if (binned)
+                    done = finish_segs(p, r, ck, ci, s_seg, T, neg, kk, m0, top_p, u, MH, hist, s_ms, s_cs, tok, st);
+                if (!done) {
+                    // compact the segments (ids without their bin tags): the
+                    // buffer becomes [0, Nc) for the general path
+                    constexpr int PERW = FSEG / 64;
+                    const int w = wave_id();
+                    const uint32_t cw = s_seg[w];
+                    uint32_t off = 0;
+#pragma unroll
+                    for (int v = 0; v < NWAVES; ++v) off += v < w ? s_seg[v] : 0u;
+                    uint32_t kv[PERW], iv[PERW];
+#pragma unroll
+                    for (int q = 0; q < PERW; ++q) {
+                        const uint32_t j = (uint32_t)(lane + 64 * q);
+                        kv[q] = j < cw ? ck[w * FSEG + j] : 0u;
+                        iv[q] = j < cw ? ci[w * FSEG + j] & ID_MASK : 0u;
+                    }
+                    __syncthreads();
+#pragma unroll
+                    for (int q = 0; q < PERW; ++q) {
+                        const uint32_t j = (uint32_t)(lane + 64 * q);
+                        if (j < cw) { ck[off + j] = kv[q]; ci[off + j] = iv[q]; }
+                    }
+                    Nfix = Nc;
+                    __syncthreads();
+                }
+            }
+            if (mode == MODE_TOPK && !overflow && !done) {
                 auto visit = [&](auto&& f) {
                     for (uint32_t j = tid; j < Nc; j += NT) f(ck[j]);
                 };
