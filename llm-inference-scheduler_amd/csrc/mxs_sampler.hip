@@ -86,35 +86,23 @@ __device__ __forceinline__ float penalize(float v, float pen) { return v > 0.0f 
 // tempered value and then tie with it.
 __device__ __forceinline__ uint32_t widen_threshold(uint32_t th, float T, bool neg)
 {
-    __shared__ uint32_t s_res;
-    if (wave_id() == 0) {
-        const int lane = lane_id();
-        const float kth = sel_inv(th, neg) / T;
-        auto pred = [&](uint32_t s) -> bool { return s >= SK_MIN && (sel_inv(s, neg) / T) >= kth; };
-        bool ok = th >= (uint32_t)lane && pred(th - (uint32_t)lane);
-        u64 mask = __ballot(ok);
-        uint32_t res;
-        if (~mask != 0ull) {
-            int j = __builtin_ctzll(~mask);        // first failing lane; lanes 0..j-1 hold
-            res = th - (uint32_t)(j - 1);
-        } else {
-            uint32_t lo = SK_MIN, hi = th - 63u;   // pred(hi) holds
-            if (pred(lo)) {
-                res = lo;
-            } else {
-                while (hi - lo > 1u) {
-                    uint32_t mid = lo + (hi - lo) / 2u;
-                    if (pred(mid)) hi = mid; else lo = mid;
-                }
-                res = hi;
-            }
-        }
-        if (lane == 0) s_res = res;
+    // every wave computes it (the same result), so no barrier is needed
+    const int lane = lane_id();
+    const float kth = sel_inv(th, neg) / T;
+    auto pred = [&](uint32_t s) -> bool { return s >= SK_MIN && (sel_inv(s, neg) / T) >= kth; };
+    const bool ok = th >= (uint32_t)lane && pred(th - (uint32_t)lane);
+    const u64 mask = __ballot(ok);
+    if (~mask != 0ull) {
+        const int j = __builtin_ctzll(~mask);        // first failing lane; lanes 0..j-1 hold
+        return th - (uint32_t)(j - 1);
     }
-    __syncthreads();
-    uint32_t r = s_res;
-    __syncthreads();
-    return r;
+    uint32_t lo = SK_MIN, hi = th - 63u;   // pred(hi) holds
+    if (pred(lo)) return lo;
+    while (hi - lo > 1u) {
+        const uint32_t mid = lo + (hi - lo) / 2u;
+        if (pred(mid)) hi = mid; else lo = mid;
+    }
+    return hi;
 }
 
 struct Reduced {
@@ -747,202 +735,167 @@ __device__ __forceinline__ u64 wave_sum_above(const T* h, u64 s, int b)
     return wave_sum64(v);
 }
 
-// Ranks of a gathered bin (n <= 64 keys in LDS, any order), one element per
-// lane: its key, mass, the number of keys above it and their mass.
+// One element of a gathered bin per lane: its key, mass, the number of the
+// bin's keys above it and their mass.
 struct Ranked {
     u64 key, w, E;
     uint32_t gt;
     bool valid;
 };
-__device__ __forceinline__ Ranked rank_gathered(const u64* keys, const u64* ws, uint32_t n)
-{
-    const uint32_t lane = (uint32_t)lane_id();
-    Ranked q{0ull, 0ull, 0ull, 0u, lane < n};
-    if (q.valid) { q.key = keys[lane]; q.w = ws[lane]; }
-    for (uint32_t i = 0; i < n; ++i) {   // broadcast reads of the gathered keys
-        const u64 o = keys[i];
-        const bool above = o > q.key;
-        q.gt += above ? 1u : 0u;
-        q.E += above ? ws[i] : 0ull;
-    }
-    return q;
-}
-
 // Input, from the kernel's pass over the segments: every buffered element
 // with l >= l_est carries its bin + 1 in bits 18 and up of its id word
-// (V <= 2^18), the others 0 there; CH / MH hold the counts and masses
-// mass_of(l - m) per bin, CS / MS per group of 32 bins.  Returns false,
-// having written nothing, when a bin holds more than 64 elements: the
-// caller then takes the general path.
+// (V <= 2^18), the others 0 there; CH holds the counts per bin (2048 bins
+// linear in d = l - m on [l_est - m, 0], monotone in the sorted order), CS
+// the counts per group of 32 bins.
+//
+// Every wave finds the bin kb of the k-th largest by itself.  CH then turns
+// into the offsets of the bins in descending order (a counting sort), and a
+// second pass places the elements of the bins >= kb (they include the top-k
+// set) there in the kept list KL, bin by bin, with their masses, which also
+// go into MH / MS.  After that pass CH[b] is the end of bin b in KL and
+// CH[b + 1] its start.  Wave 0 resolves the k-th, the top-p cut and the draw,
+// each from the bin that holds it, read directly from KL.  Returns false,
+// having written nothing but KL and CH, when a needed bin holds more than 64
+// elements or KL would exceed KL_CAP: the caller then takes the general path.
 constexpr int TAG_SHIFT = 18;
 constexpr uint32_t ID_MASK = (1u << TAG_SHIFT) - 1u;
 static_assert(MXS_MAX_VOCAB <= (1 << TAG_SHIFT), "ids and bin tags share a word");
+constexpr int KL_CAP = 2048;
+static_assert(KL_CAP * 16 <= KF_MH - KF_BM, "the kept list fits where the history bitmap was");
 
 __device__ __forceinline__ bool finish_segs(const Params& p, int r, const uint32_t* ck, const uint32_t* ci,
                                             const uint32_t* seg, float T, bool neg, uint32_t kk, float m,
-                                            float top_p, float u, const u64* MH, const uint32_t* CH,
-                                            const u64* MS, const uint32_t* CS, int64_t& tok, int32_t& st)
+                                            float top_p, float u, u64* MH, uint32_t* CH, u64* MS,
+                                            const uint32_t* CS, u64* KL, int64_t& tok, int32_t& st)
 {
-    __shared__ u64 g_key[2][64], g_w[2][64];
-    __shared__ uint32_t g_n[2];
-    __shared__ int g_req[2];     // bins to gather next (-1: none)
     __shared__ int g_fail;
     __shared__ u64 g_tok, g_wk, g_cut;
     __shared__ uint32_t g_vkk;
     __shared__ int g_st, g_bounded;
     const int wv = wave_id(), lane = lane_id();
+    const int tid = threadIdx.x;
     const uint32_t cw = seg[wv];
     const uint32_t* wck = ck + wv * FSEG;
     const uint32_t* wci = ci + wv * FSEG;
 
-    // Wave 0 resolves the row in phases; each phase names the bins that the
-    // workgroup gathers for the next one.
-    enum { PH_K, PH_CUT, PH_DRAW, PH_DONE };
-    int phase = PH_K;
-    u64 cs = 0, ms = 0;      // this lane's group of 32 bins
-    u64 Ak = 0, W = 0, Wk = 0, t = 0, D = 0, Ac = 0, Ad = 0, cutkey = 0, nabove = 0;
-    uint32_t vkk = 0;
-    int kb = 0, bd = -1;
-    bool bounded = false;
-    int32_t rst = MXS_ROW_OK;
-    u64 dkey = 0;
-    if (threadIdx.x == 0) { g_n[0] = 0; g_n[1] = 0; g_req[1] = -1; g_fail = 0; }
+    // the k-th's bin, by every wave; the size of KL
+    const WHit hk = wave_find_desc<uint32_t>(CH, (u64)CS[lane], (u64)(kk - 1u));
+    const int kb = hk.bin;
+    const uint32_t nkb = CH[kb];
+    if (hk.above + nkb > (u64)KL_CAP || nkb > 64u) return false;
+    // CH -> exclusive offsets in descending bin order: this thread's 4 bins
+    // are 2047 - 4 tid down to 2044 - 4 tid
+    {
+        uint32_t c[4], sum = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { c[i] = CH[2047 - 4 * tid - i]; sum += c[i]; }
+        uint32_t total;
+        uint32_t off = block_incl_scan<uint32_t>(sum, &total) - sum;   // (its barriers end the reads above)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { CH[2047 - 4 * tid - i] = off; off += c[i]; }
+    }
+    __syncthreads();
+    // the bins from kb up: masses, and their places in KL
+    const uint32_t tkb = (uint32_t)kb + 1u;
+    for (uint32_t j = (uint32_t)lane; j < cw; j += 64) {
+        const uint32_t word = wci[j];
+        const uint32_t tag = word >> TAG_SHIFT;
+        if (tag >= tkb) {
+            const float l = sel_inv(wck[j], neg) / T;
+            const u64 w = mass_of(l - m);
+            const uint32_t b = tag - 1u;
+            atomicAdd(&MH[b], w);
+            atomicAdd(&MS[b >> 5], w);
+            const uint32_t at = atomicAdd(&CH[b], 1u);
+            KL[2 * at] = ((u64)vkey(l) << 32) | (u64)(0xFFFFFFFFu - (word & ID_MASK));
+            KL[2 * at + 1] = w;
+        }
+    }
+    __syncthreads();
+    const uint32_t nk = CH[kb];   // (the end of kb: the size of KL)
     if (wv == 0) {
-        cs = CS[lane];
-        ms = MS[lane];
-        const WHit hk = wave_find_desc<uint32_t>(CH, cs, (u64)(kk - 1u));
-        kb = hk.bin;
-        nabove = hk.above;
-        Ak = wave_sum_above<u64>(MH, ms, kb);
-        if (lane == 0) g_req[0] = kb;
-    }
-    for (int round = 0;; ++round) {   // (wave 0 is done, or has failed, within three rounds)
-        __syncthreads();
-        const int rq0 = g_req[0], rq1 = g_req[1];
-        if (g_fail) return false;
-        if (rq0 < 0 && rq1 < 0) break;
-        const uint32_t tg0 = (uint32_t)(rq0 + 1), tg1 = (uint32_t)(rq1 + 1);
-        for (uint32_t j = (uint32_t)lane; j < cw; j += 64) {   // gather the requested bins
-            const uint32_t word = wci[j];
-            const uint32_t tag = word >> TAG_SHIFT;
-            if (tag != 0u && (tag == tg0 || tag == tg1)) {
-                const float l = sel_inv(wck[j], neg) / T;
-                const int li = tag == tg0 ? 0 : 1;
-                const uint32_t slot = atomicAdd(&g_n[li], 1u);
-                if (slot < 64u) {
-                    g_key[li][slot] = ((u64)vkey(l) << 32) | (u64)(0xFFFFFFFFu - (word & ID_MASK));
-                    g_w[li][slot] = mass_of(l - m);
+        bool fail = false;
+        const u64 ms = MS[lane];
+        const u64 Ak = wave_sum_above<u64>(MH, ms, kb);
+        // bin b's elements, one per lane, ranked
+        auto load_bin = [&](int b) -> Ranked {
+            const uint32_t e = CH[b], s0 = b == 2047 ? 0u : CH[b + 1];
+            const uint32_t n = e - s0;
+            if (n > 64u) fail = true;
+            Ranked q{0ull, 0ull, 0ull, 0u, (uint32_t)lane < n};
+            if (q.valid) { q.key = KL[2 * (s0 + lane)]; q.w = KL[2 * (s0 + lane) + 1]; }
+            // ranks by broadcast reads of the bin's keys, four at a time
+            // (entries past the bin read as zero keys, which are below all)
+            for (uint32_t i = 0; i < n; i += 4) {
+                u64 o[4], ow[4];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const bool in = i + c < n;
+                    o[c] = in ? KL[2 * (s0 + i + c)] : 0ull;
+                    ow[c] = in ? KL[2 * (s0 + i + c) + 1] : 0ull;
+                }
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const bool above = o[c] > q.key;
+                    q.gt += above ? 1u : 0u;
+                    q.E += above ? ow[c] : 0ull;
                 }
             }
-        }
-        __syncthreads();
-        const uint32_t n0 = g_n[0], n1 = g_n[1];
-        if (n0 > 64u || n1 > 64u) return false;
-        __syncthreads();   // (every wave has read the counts)
-        if (wv == 0) {
-            const Ranked q0 = rank_gathered(g_key[0], g_w[0], n0);
-            const Ranked q1 = rank_gathered(g_key[1], g_w[1], n1);
-            int next0 = -1, next1 = -1;
-            bool fail = false;
-            // the key, mass and mass before it of the element of list q whose
-            // mass interval, offset by A, holds x
-            auto pick = [&](const Ranked& q, bool elig, u64 A, u64 x, u64& key, u64& E, u64& w) {
-                const u64 mk = __ballot(elig && A + q.E <= x && x < A + q.E + q.w);
-                if (!mk) { fail = true; return; }
-                const int l0 = __builtin_ctzll(mk);
-                key = readlane64(q.key, l0);
-                E = A + readlane64(q.E, l0);
-                w = readlane64(q.w, l0);
-            };
-            // the draw once Wk is known: from list q (offset A) or a bin above it
-            auto draw_from = [&](const Ranked& q, bool elig, u64 A) {
-                D = floor_mul(clamp_uniform(u), Wk);   // sampling.py:69
-                if (D >= A) {
-                    u64 E, w;
-                    pick(q, elig, A, D, dkey, E, w);
-                    phase = PH_DONE;
-                } else {
-                    const WHit hd = wave_find_desc<u64>(MH, ms, D);
-                    bd = hd.bin;
-                    Ad = hd.above;
-                    next0 = bd;
-                    phase = PH_DRAW;
-                }
-            };
-            if (phase == PH_K) {
-                // sampling.py:52-54: the k-th largest of the bin; its value ties stay
-                const uint32_t rk = (kk - 1u) - (uint32_t)nabove;
-                const u64 mk = __ballot(q0.valid && q0.gt == rk);
-                if (!mk) fail = true;
-                vkk = (uint32_t)(readlane64(q0.key, mk ? __builtin_ctzll(mk) : 0) >> 32);
-                const bool kept = q0.valid && (uint32_t)(q0.key >> 32) >= vkk;
-                W = Ak + wave_sum64(kept ? q0.w : 0ull);
-                Wk = W;
-                if (top_p < 1.0f && !(top_p > 0.0f)) {
-                    rst = MXS_ROW_EMPTY_NUCLEUS;
-                    phase = PH_DONE;
-                } else if (top_p < 1.0f) {   // sampling.py:56-63
-                    t = ceil_mul(top_p, W) - 1;
-                    bounded = true;
-                    if (t >= Ak) {
-                        u64 E, w;
-                        pick(q0, kept, Ak, t, cutkey, E, w);
-                        Wk = E + w;
-                        draw_from(q0, kept, Ak);
-                    } else {
-                        const WHit hc = wave_find_desc<u64>(MH, ms, t);
-                        Ac = hc.above;
-                        next0 = hc.bin;
-                        phase = PH_CUT;
-                        // Wk will lie in (Ac, Ac + MH[cut's bin]]: when the draw
-                        // position lands in one bin above the cut's bin at both
-                        // ends, gather that bin now as well
-                        const float uc = clamp_uniform(u);
-                        const u64 Dlo = floor_mul(uc, Ac + 1), Dhi = floor_mul(uc, Ac + MH[hc.bin]);
-                        if (Dhi < Ac) {
-                            const WHit h1 = wave_find_desc<u64>(MH, ms, Dlo);
-                            const WHit h2 = wave_find_desc<u64>(MH, ms, Dhi);
-                            if (h1.bin == h2.bin) { bd = h1.bin; Ad = h1.above; next1 = bd; }
-                        }
-                    }
-                } else {
-                    draw_from(q0, kept, Ak);
-                }
-            } else if (phase == PH_CUT) {   // the cut's bin lies wholly in the top-k set
-                u64 E, w;
-                pick(q0, q0.valid, Ac, t, cutkey, E, w);
+            return q;
+        };
+        // sampling.py:52-54: the k-th largest of its bin; its value ties stay
+        Ranked q = load_bin(kb);
+        int qb = kb;
+        const uint32_t rk = (kk - 1u) - (uint32_t)hk.above;
+        const u64 mk = __ballot(q.valid && q.gt == rk);
+        if (!mk) fail = true;
+        const uint32_t vkk = (uint32_t)(readlane64(q.key, mk ? __builtin_ctzll(mk) : 0) >> 32);
+        const bool kept = q.valid && (uint32_t)(q.key >> 32) >= vkk;
+        const u64 W = Ak + wave_sum64(kept ? q.w : 0ull);
+        // the element at mass position x < W: its key, the mass before it, its mass
+        auto pick_at = [&](u64 x, u64& key, u64& E, u64& w) {
+            int b = kb;
+            u64 A = Ak;
+            if (x < Ak) {
+                const WHit h = wave_find_desc<u64>(MH, ms, x);
+                b = h.bin;
+                A = h.above;
+            }
+            if (b != qb) { q = load_bin(b); qb = b; }
+            const bool elig = b == kb ? (q.valid && (uint32_t)(q.key >> 32) >= vkk) : q.valid;
+            const u64 hm = __ballot(elig && A + q.E <= x && x < A + q.E + q.w);
+            if (!hm) { fail = true; return; }
+            const int l0 = __builtin_ctzll(hm);
+            key = readlane64(q.key, l0);
+            E = A + readlane64(q.E, l0);
+            w = readlane64(q.w, l0);
+        };
+        int32_t rst = MXS_ROW_OK;
+        u64 Wk = W, cutkey = 0, dkey = 0;
+        bool bounded = false;
+        if (top_p < 1.0f && !(top_p > 0.0f)) {
+            rst = MXS_ROW_EMPTY_NUCLEUS;
+        } else {
+            u64 E, w;
+            if (top_p < 1.0f) {   // sampling.py:56-63
+                bounded = true;
+                pick_at(ceil_mul(top_p, W) - 1, cutkey, E, w);
                 Wk = E + w;
-                D = floor_mul(clamp_uniform(u), Wk);
-                if (bd >= 0 && D < Ac) {   // the bin gathered alongside
-                    pick(q1, q1.valid, Ad, D, dkey, E, w);
-                    phase = PH_DONE;
-                } else {
-                    draw_from(q0, q0.valid, Ac);
-                }
-            } else if (phase == PH_DRAW) {
-                u64 E, w;
-                pick(q0, q0.valid, Ad, D, dkey, E, w);
-                phase = PH_DONE;
             }
-            if (round >= 2 && phase != PH_DONE) fail = true;
-            if (lane == 0) {
-                g_n[0] = 0;
-                g_n[1] = 0;
-                g_req[0] = phase == PH_DONE ? -1 : next0;
-                g_req[1] = phase == PH_DONE ? -1 : next1;
-                if (fail) g_fail = 1;
-                if (phase == PH_DONE) {
-                    g_tok = dkey;
-                    g_wk = Wk;
-                    g_cut = cutkey;
-                    g_vkk = vkk;
-                    g_st = rst;
-                    g_bounded = bounded ? 1 : 0;
-                }
-            }
+            pick_at(floor_mul(clamp_uniform(u), Wk), dkey, E, w);   // sampling.py:69
+        }
+        if (lane == 0) {
+            g_fail = fail ? 1 : 0;
+            g_tok = dkey;
+            g_wk = Wk;
+            g_cut = cutkey;
+            g_vkk = vkk;
+            g_st = rst;
+            g_bounded = bounded ? 1 : 0;
         }
     }
-    // (the loop ends at a barrier after wave 0's last phase)
+    __syncthreads();
+    if (g_fail) return false;
     st = g_st;
     if (st != MXS_ROW_OK) { tok = -1; return true; }
     tok = (int64_t)(0xFFFFFFFFu - (uint32_t)g_tok);
@@ -951,15 +904,10 @@ __device__ __forceinline__ bool finish_segs(const Params& p, int r, const uint32
         const uint32_t vk_k = g_vkk;
         const bool bnd = g_bounded != 0;
         float* out = p.out_probs + (size_t)r * (size_t)p.V;
-        for (uint32_t j = (uint32_t)lane; j < cw; j += 64) {
-            const uint32_t word = wci[j];
-            if (word >> TAG_SHIFT) {
-                const float l = sel_inv(wck[j], neg) / T;
-                const uint32_t id = word & ID_MASK;
-                const u64 key = ((u64)vkey(l) << 32) | (u64)(0xFFFFFFFFu - id);
-                if (bnd ? key >= cut : (uint32_t)(key >> 32) >= vk_k)
-                    out[id] = (float)((double)mass_of(l - m) / (double)wkk);
-            }
+        for (uint32_t i = (uint32_t)tid; i < nk; i += NT) {
+            const u64 key = KL[2 * i];
+            if (bnd ? key >= cut : (uint32_t)(key >> 32) >= vk_k)
+                out[0xFFFFFFFFu - (uint32_t)key] = (float)((double)KL[2 * i + 1] / (double)wkk);
         }
     }
     return true;
@@ -1494,6 +1442,8 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
     __shared__ uint32_t s_seg[NWAVES];          // entries per buffer segment
     __shared__ uint32_t s_ovf;                  // a segment ran full
     __shared__ uint32_t s_nh;                   // distinct history ids listed in hl
+    __shared__ u64 s_ms[64];                    // masses per group of 32 bins
+    __shared__ uint32_t s_cs[64];               // counts per group of 32 bins
 
     const int tid = threadIdx.x, lane = lane_id();
     const int r = blockIdx.x;
@@ -1545,8 +1495,10 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
     int32_t st = MXS_ROW_OK;
 
     const bool sampled = mode == MODE_TOPK && V >= FAST_MIN_V;
-    if (sampled)
+    if (sampled) {
         for (int b = tid; b < 2048; b += NT) hist[b] = 0;
+        if (tid < 64) s_cs[tid] = 0;
+    }
     // With 1 <= pen < inf and T > 0 the penalty never raises a selection
     // key, so a top-k row's stream may compare raw keys: the raw hits include
     // every penalized hit.  Buffered history ids get their penalized keys
@@ -1569,10 +1521,13 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
     uint32_t* hl = (uint32_t*)(smem + KF_HL);
     if (tid == 0) s_nh = 0;
     if (pen_on) {
+        // (unconditional loads, clamped into the row's history: writing a
+        // default into a register with a load pending would wait for every
+        // load in flight; build_bitmap skips the clamped ones)
 #pragma unroll
         for (int q = 0; q < HB; ++q) {
             const int h = h0 + tid + q * NT;
-            hv[q] = h < h1 ? p.hids[h] : 0;
+            hv[q] = p.hids[h < h1 ? h : h1 - 1];
         }
         const int words = (V + 31) >> 5;
         for (int w = tid; w < words; w += NT) bm[w] = 0;
@@ -1643,8 +1598,6 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
         float m0 = 0.0f, lest = 0.0f;
         Reduced rd{0u, 0xFFFFFFFFu, 0u};
         u64* MH = (u64*)(smem + KF_MH);
-        __shared__ u64 s_ms[64];
-        __shared__ uint32_t s_cs[64];
         __shared__ uint32_t s_r[5][NWAVES];
         if (mode == MODE_TOPK) {
             // 1. A conservative estimate of the k-th largest key from a strided
@@ -1671,9 +1624,14 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                 const uint32_t span = sr.max - sr.min;
                 const int sh = span >= 2048u ? (32 - __builtin_clz(span)) - 11 : 0;
 #pragma unroll
-                for (int q = 0; q < NS; ++q) atomicAdd(&hist[(sk4[q] - sr.min) >> sh], 1u);
+                for (int q = 0; q < NS; ++q) {
+                    const uint32_t b = (sk4[q] - sr.min) >> sh;
+                    atomicAdd(&hist[b], 1u);
+                    atomicAdd(&s_cs[b >> 5], 1u);
+                }
                 __syncthreads();
-                const BinHit hb = find_desc<uint32_t>(hist, 2048, (u64)(js - 1u));
+                // (every wave finds the bin by itself)
+                const WHit hb = wave_find_desc<uint32_t>(hist, (u64)s_cs[lane], (u64)(js - 1u));
                 est = sr.min + ((uint32_t)hb.bin << sh);
                 if (est < SK_MIN) est = SK_MIN;
                 theta = widen_threshold(est, T, neg);
@@ -1771,14 +1729,10 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                     if (binned) {
                         const float l = sel_inv(key, neg) / T;
                         if (l >= lest) {
-                            const float d = l - m0;
-                            const float f = (d - dlo) * scale;
+                            const float f = ((l - m0) - dlo) * scale;
                             const uint32_t b = f < 2047.0f ? (uint32_t)f : 2047u;
-                            const u64 wgt = mass_of(d);
                             atomicAdd(&hist[b], 1u);
-                            atomicAdd(&MH[b], wgt);
                             atomicAdd(&s_cs[b >> 5], 1u);
-                            atomicAdd(&s_ms[b >> 5], wgt);
                             wci[j] = id | ((b + 1u) << TAG_SHIFT);
                         }
                     }
@@ -1808,22 +1762,18 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                     const float dlo2 = lest - m0;
                     const float scale2 = 2047.0f / -dlo2;
                     binned = dlo2 < 0.0f && dlo2 > -INFINITY && __builtin_isfinite(scale2) && __builtin_isfinite(m0);
-                    for (int b = tid; b < 2048; b += NT) { MH[b] = 0; hist[b] = 0; }
-                    if (tid < 64) { s_cs[tid] = 0; s_ms[tid] = 0; }
+                    for (int b = tid; b < 2048; b += NT) hist[b] = 0;
+                    if (tid < 64) s_cs[tid] = 0;
                     __syncthreads();
                     for (uint32_t j = (uint32_t)lane; j < cw; j += 64) {
                         const uint32_t id = wci[j] & ID_MASK;
                         uint32_t word = id;
                         const float l = sel_inv(wck[j], neg) / T;
                         if (binned && l >= lest) {
-                            const float d = l - m0;
-                            const float f = (d - dlo2) * scale2;
+                            const float f = ((l - m0) - dlo2) * scale2;
                             const uint32_t b = f < 2047.0f ? (uint32_t)f : 2047u;
-                            const u64 wgt = mass_of(d);
                             atomicAdd(&hist[b], 1u);
-                            atomicAdd(&MH[b], wgt);
                             atomicAdd(&s_cs[b >> 5], 1u);
-                            atomicAdd(&s_ms[b >> 5], wgt);
                             word = id | ((b + 1u) << TAG_SHIFT);
                         }
                         wci[j] = word;
@@ -1941,8 +1891,18 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
             uint32_t thk = 0;
             bool thk_known = false;
             if (segs) {
-                if (binned)
-                    done = finish_segs(p, r, ck, ci, s_seg, T, neg, kk, m0, top_p, u, MH, hist, s_ms, s_cs, tok, st);
+                if (binned) {
+                    // (its kept list goes where the history bitmap was)
+                    done = finish_segs(p, r, ck, ci, s_seg, T, neg, kk, m0, top_p, u, MH, hist, s_ms, s_cs,
+                                       (u64*)(smem + KF_BM), tok, st);
+                    if (!done && pen_on) {   // the general path needs the bitmap again
+                        const int words = (V + 31) >> 5;
+                        for (int w2 = tid; w2 < words; w2 += NT) bm[w2] = 0;
+                        __syncthreads();
+                        (void)build_bitmap();
+                        __syncthreads();
+                    }
+                }
                 if (!done) {
                     // compact the segments (ids without their bin tags): the
                     // buffer becomes [0, Nc) for the general path
