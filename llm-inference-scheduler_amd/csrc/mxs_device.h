@@ -207,6 +207,10 @@ __device__ __forceinline__ uint32_t wave_or_u32(uint32_t v)
 {
     return lane63(wave_prefix_op<uint32_t>(v, 0u, [](uint32_t a, uint32_t b) { return a | b; }));
 }
+__device__ __forceinline__ uint32_t wave_prefix_u32(uint32_t v)
+{
+    return wave_prefix_op<uint32_t>(v, 0u, [](uint32_t a, uint32_t b) { return a + b; });
+}
 __device__ __forceinline__ u64 wave_prefix_u64(u64 v)
 {
     return wave_prefix_op<u64>(v, 0ull, [](u64 a, u64 b) { return a + b; });

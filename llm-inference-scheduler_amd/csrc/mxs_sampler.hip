@@ -1644,45 +1644,41 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                 uint32_t* wck = ck + w * FSEG;
                 uint32_t* wci = ci + w * FSEG;
                 uint32_t cw = 0;
+                // Each lane appends its own hits in slot order at its offset
+                // in the wave's segment (an exclusive prefix of the lanes' hit
+                // counts); a slot without a hit writes a per-lane dummy word
+                // at the segment's end instead, so the appends need no branch.
                 uint32_t tk[FPT];   // this tile's keys
-                u64 wm[FPT];        // wave ballots of the hits, per slot
-#pragma unroll
-                for (int i = 0; i < FPT; ++i) wm[i] = 0;
+                uint32_t hm = 0;    // this lane's hits in the tile, one bit per slot
+                constexpr uint32_t SEG_USE = FSEG - 64;   // [SEG_USE, FSEG): the dummy words
                 rs.run_pen(bm, pen_on && !defer, pen,
                     [&](int i, int, float x) {
                         const uint32_t sk = selkey(x, neg);
                         omax = sk > omax ? sk : omax;
                         omin = sk < omin ? sk : omin;
                         tk[i] = sk;
-                        wm[i] = __ballot(sk >= theta);
+                        hm |= (sk >= theta ? 1u : 0u) << i;
                     },
                     [&](auto&& id) -> bool {
-                        // the ballots as lane 0 holds them (a slot past the row's end
-                        // skips a wave's highest lanes)
-                        uint32_t tot = 0;
-#pragma unroll
-                        for (int i = 0; i < FPT; ++i) {
-                            wm[i] = ((u64)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(wm[i] >> 32)) << 32) |
-                                    (u64)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)wm[i]);
-                            tot += (uint32_t)__builtin_popcountll(wm[i]);
-                        }
-                        if (cw + tot > (uint32_t)FSEG) {
+                        const uint32_t c = (uint32_t)__builtin_popcount(hm);
+                        const uint32_t incl = wave_prefix_u32(c);
+                        const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+                        if (cw + tot > SEG_USE) {
                             if (lane == 0) __hip_atomic_store(&s_ovf, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
                             return true;
                         }
+                        uint32_t o = cw + incl - c;
+                        const uint32_t dummy = SEG_USE + (uint32_t)lane;
 #pragma unroll
                         for (int i = 0; i < FPT; ++i) {
-                            const u64 m = wm[i];
-                            if (m) {
-                                if ((m >> lane) & 1ull) {
-                                    const uint32_t o = cw + lanes_below(m);
-                                    wck[o] = tk[i];
-                                    wci[o] = (uint32_t)id(i);
-                                }
-                                cw += (uint32_t)__builtin_popcountll(m);
-                            }
-                            wm[i] = 0;
+                            const uint32_t h = (hm >> i) & 1u;
+                            const uint32_t a = h ? o : dummy;
+                            wck[a] = tk[i];
+                            wci[a] = (uint32_t)id(i);
+                            o += h;
                         }
+                        hm = 0;
+                        cw += tot;
                         return __hip_atomic_load(&s_ovf, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0u;
                     });
                 if (lane == 0) s_seg[w] = cw;
