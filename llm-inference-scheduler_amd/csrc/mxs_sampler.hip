@@ -2,15 +2,16 @@
 //
 // Reference chain: mini_engine/sampling.py:30-69, one [vocab] row per call.
 // Here one call samples a whole [B, V] batch with one launch of k_fused: one
-// workgroup per row (about 157 KB of LDS, so one row per CU), which streams
+// workgroup per row (152 KB of dynamic LDS, so one row per CU), which streams
 // the row from HBM once and finishes it on chip:
 //   greedy     a packed (key, index) maximum;
 //   top-k      candidates above a sampled, then verified, lower bound on the
 //              k-th largest key, kept in LDS; exact k-th, top-p cut and draw
-//              from the candidates;
-//   top-k off  a mass pass over the row (from cache), then the cut's and the
-//              draw's bins gathered and ranked;
-// with a multi-level fallback (finish_large) for massive ties.
+//              from a counting sort of the candidates by mass bins;
+//   top-k off  a mass pass over the row, then the cut's and the draw's bins
+//              gathered and ranked;
+// with general paths (compaction and exact select, finish_large) for what
+// the fast ones decline: failed bounds, full buffers, heavy ties.
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 #include <stddef.h>
@@ -735,6 +736,21 @@ __device__ __forceinline__ u64 wave_sum_above(const T* h, u64 s, int b)
     return wave_sum64(v);
 }
 
+// S[g] = the sum of H[32 g, 32 g + 32) for the 64 groups of a 2048-bin
+// histogram, by the whole workgroup: 4 bins per thread, then sums over each
+// 8-lane group by DPP; ends with a barrier.
+template <typename T>
+__device__ __forceinline__ void group_sums(const T* H, T* S)
+{
+    const int tid = threadIdx.x;
+    T v = H[4 * tid] + H[4 * tid + 1] + H[4 * tid + 2] + H[4 * tid + 3];
+    v += dpp_step(v, (T)0, 0);   // lanes i-1, i-2, i-4 within the row:
+    v += dpp_step(v, (T)0, 1);   // lane 8g + 7 then holds lanes 8g .. 8g + 7
+    v += dpp_step(v, (T)0, 2);
+    if ((tid & 7) == 7) S[tid >> 3] = v;
+    __syncthreads();
+}
+
 // One element of a gathered bin per lane: its key, mass, the number of the
 // bin's keys above it and their mass.
 struct Ranked {
@@ -797,21 +813,44 @@ __device__ __forceinline__ bool finish_segs(const Params& p, int r, const uint32
     __syncthreads();
     // the bins from kb up: masses, and their places in KL
     const uint32_t tkb = (uint32_t)kb + 1u;
-    for (uint32_t j = (uint32_t)lane; j < cw; j += 64) {
-        const uint32_t word = wci[j];
-        const uint32_t tag = word >> TAG_SHIFT;
-        if (tag >= tkb) {
-            const float l = sel_inv(wck[j], neg) / T;
-            const u64 w = mass_of(l - m);
-            const uint32_t b = tag - 1u;
-            atomicAdd(&MH[b], w);
-            atomicAdd(&MS[b >> 5], w);
-            const uint32_t at = atomicAdd(&CH[b], 1u);
-            KL[2 * at] = ((u64)vkey(l) << 32) | (u64)(0xFFFFFFFFu - (word & ID_MASK));
-            KL[2 * at + 1] = w;
+    // four entries per lane at a time: loads, then arithmetic, then the
+    // atomics, then the placements, each issued together
+    for (uint32_t j0 = (uint32_t)lane; j0 < cw; j0 += 256) {
+        uint32_t word[4], skv[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t j = j0 + 64u * q < cw ? j0 + 64u * q : j0;
+            word[q] = wci[j];
+            skv[q] = wck[j];
+        }
+        bool in[4];
+        float lq[4];
+        u64 wq[4];
+        uint32_t at[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            in[q] = j0 + 64u * q < cw && (word[q] >> TAG_SHIFT) >= tkb;
+            lq[q] = sel_inv(skv[q], neg) / T;
+            wq[q] = in[q] ? mass_of(lq[q] - m) : 0ull;
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            if (in[q]) {
+                const uint32_t b = (word[q] >> TAG_SHIFT) - 1u;
+                atomicAdd(&MH[b], wq[q]);
+                at[q] = atomicAdd(&CH[b], 1u);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            if (in[q]) {
+                KL[2 * at[q]] = ((u64)vkey(lq[q]) << 32) | (u64)(0xFFFFFFFFu - (word[q] & ID_MASK));
+                KL[2 * at[q] + 1] = wq[q];
+            }
         }
     }
     __syncthreads();
+    group_sums<u64>(MH, MS);
     const uint32_t nk = CH[kb];   // (the end of kb: the size of KL)
     if (wv == 0) {
         bool fail = false;
@@ -917,17 +956,17 @@ __device__ __forceinline__ bool finish_segs(const Params& p, int r, const uint32
 //
 // One workgroup per row, the whole chain in one launch.  The row streams from
 // HBM once, in 128-bit loads with two tiles of FTILE logits in flight per
-// workgroup; the penalty is applied from an LDS bitmap of the row's history.
+// workgroup; the penalty is applied from an LDS bitmap of the row's history
+// (inline, or to the buffered candidates afterwards).
 //   greedy  a packed (key, index) maximum;
-//   top-k   every element whose selection key reaches a running lower bound
-//           theta on the row's k-th largest key is kept in an LDS buffer.
-//           When the buffer nears capacity, theta rises to the lower edge of
-//           the histogram bin holding the k-th largest buffered key (k
-//           buffered elements are at least that large, so the bound stays
-//           valid), widened over the rounding of x / T, and the buffer is
-//           compacted.  The exact k-th key, the top-p cut and the draw then
-//           come from the buffer alone;
-//   other   the row's extreme keys, then the multi-pass path.
+//   top-k   every element whose selection key reaches a lower bound theta on
+//           the row's k-th largest key (from a sample, checked afterwards)
+//           is appended to its wave's LDS segment; the segments are then
+//           binned by mass and counting-sorted (finish_segs).  When the
+//           bound fails or a segment fills, the row streams again into one
+//           shared buffer whose bound rises by compaction whenever it nears
+//           capacity;
+//   other   the row's extreme keys, then the top-p-only path.
 
 // Streams the row in tiles of FTILE logits, FTILE / NT = 16 per thread:
 // elem(i, e, x) for slot i in [0, 16) of this thread's share of the tile,
@@ -1685,7 +1724,6 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                 bool bad = false;
                 if (late_bm) bad = build_bitmap();
                 for (int b = tid; b < 2048; b += NT) { MH[b] = 0; hist[b] = 0; }
-                if (tid < 64) { s_cs[tid] = 0; s_ms[tid] = 0; }
                 {
                     const uint32_t a2 = wave_max_u32(omax), a3 = wave_min_u32(omin);
                     if (lane == 0) { s_r[2][w] = a2; s_r[3][w] = a3; }
@@ -1713,23 +1751,35 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                 const float scale = 2047.0f / -dlo;
                 binned = dlo < 0.0f && dlo > -INFINITY && __builtin_isfinite(scale) && __builtin_isfinite(m0);
                 uint32_t cmx = 0, nr = 0;
-                for (uint32_t j = (uint32_t)lane; j < cw; j += 64) {
-                    uint32_t key = wck[j];
-                    const uint32_t id = wci[j];
-                    if (defer && ((bm[id >> 5] >> (id & 31)) & 1u)) {
-                        key = okey(penalize(okey_inv(key), pen));
-                        wck[j] = key;
+                // four entries per lane at a time, their loads issued together
+                for (uint32_t j0 = (uint32_t)lane; j0 < cw; j0 += 256) {
+                    uint32_t key[4], id[4], bw[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const uint32_t j = j0 + 64u * q < cw ? j0 + 64u * q : j0;
+                        key[q] = wck[j];
+                        id[q] = wci[j];
                     }
-                    cmx = key > cmx ? key : cmx;
-                    nr += key >= est ? 1u : 0u;
-                    if (binned) {
-                        const float l = sel_inv(key, neg) / T;
-                        if (l >= lest) {
-                            const float f = ((l - m0) - dlo) * scale;
-                            const uint32_t b = f < 2047.0f ? (uint32_t)f : 2047u;
-                            atomicAdd(&hist[b], 1u);
-                            atomicAdd(&s_cs[b >> 5], 1u);
-                            wci[j] = id | ((b + 1u) << TAG_SHIFT);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) bw[q] = defer ? bm[id[q] >> 5] : 0u;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const uint32_t j = j0 + 64u * q;
+                        if (j >= cw) continue;
+                        if ((bw[q] >> (id[q] & 31)) & 1u) {
+                            key[q] = okey(penalize(okey_inv(key[q]), pen));
+                            wck[j] = key[q];
+                        }
+                        cmx = key[q] > cmx ? key[q] : cmx;
+                        nr += key[q] >= est ? 1u : 0u;
+                        if (binned) {
+                            const float l = sel_inv(key[q], neg) / T;
+                            if (l >= lest) {
+                                const float f = ((l - m0) - dlo) * scale;
+                                const uint32_t b = f < 2047.0f ? (uint32_t)f : 2047u;
+                                atomicAdd(&hist[b], 1u);
+                                wci[j] = id[q] | ((b + 1u) << TAG_SHIFT);
+                            }
                         }
                     }
                 }
@@ -1759,7 +1809,6 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                     const float scale2 = 2047.0f / -dlo2;
                     binned = dlo2 < 0.0f && dlo2 > -INFINITY && __builtin_isfinite(scale2) && __builtin_isfinite(m0);
                     for (int b = tid; b < 2048; b += NT) hist[b] = 0;
-                    if (tid < 64) s_cs[tid] = 0;
                     __syncthreads();
                     for (uint32_t j = (uint32_t)lane; j < cw; j += 64) {
                         const uint32_t id = wci[j] & ID_MASK;
@@ -1769,7 +1818,6 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                             const float f = ((l - m0) - dlo2) * scale2;
                             const uint32_t b = f < 2047.0f ? (uint32_t)f : 2047u;
                             atomicAdd(&hist[b], 1u);
-                            atomicAdd(&s_cs[b >> 5], 1u);
                             word = id | ((b + 1u) << TAG_SHIFT);
                         }
                         wci[j] = word;
@@ -1888,6 +1936,7 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
             bool thk_known = false;
             if (segs) {
                 if (binned) {
+                    group_sums<uint32_t>(hist, s_cs);
                     // (its kept list goes where the history bitmap was)
                     done = finish_segs(p, r, ck, ci, s_seg, T, neg, kk, m0, top_p, u, MH, hist, s_ms, s_cs,
                                        (u64*)(smem + KF_BM), tok, st);
