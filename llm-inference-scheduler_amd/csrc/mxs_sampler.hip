@@ -1258,17 +1258,19 @@ __device__ __forceinline__ SetPick pick_in_set(u64* keys, int n, u64 t, float m,
     return res;
 }
 
-// Smallest s in [lo, hi] with pred(s), for pred monotone (false, then true)
-// and pred(hi) true; called by a whole wave, 64 probes per step.
+// Smallest s in [lo, hi] with pred(s), for pred monotone (false, then true);
+// hi + 1 when pred(hi) is false.  Called by a whole wave, 64 probes per step;
+// every step narrows [lo, hi], so it ends within 6 steps per 32 bits.
 template <class Pred>
 __device__ __forceinline__ uint32_t wave_first_true(uint32_t lo, uint32_t hi, Pred pred)
 {
     const uint32_t lane = (uint32_t)lane_id();
+    if (!__ballot(lane == 0u && pred(hi))) return hi + 1u;
     while (lo < hi) {
         const u64 span = (u64)(hi - lo);
         const uint32_t pt = lo + (uint32_t)((span * (lane + 1u)) >> 6);   // lane 63 probes hi
         const u64 msk = __ballot(pred(pt));
-        const int f = __builtin_ctzll(msk);
+        const int f = __builtin_ctzll(msk);   // (msk != 0: pred(hi) holds and lane 63 probes hi)
         const uint32_t nhi = (uint32_t)__builtin_amdgcn_readlane((int)pt, f);
         const uint32_t nlo = f > 0 ? (uint32_t)__builtin_amdgcn_readlane((int)pt, f - 1) + 1u : lo;
         lo = nlo;

@@ -262,3 +262,21 @@ def test_parity_tiny_vocabularies(oracle, cuda, V):
     ref = run_oracle(oracle, w)
     tok, st, probs = run_gpu(w, cuda)
     check(w, ref, tok, st, probs)
+
+
+@pytest.mark.parametrize("V", [7, 1000, 4099, 8192])
+def test_parity_constant_rows_top_p_only(oracle, cuda, V):
+    """Rows whose values are all equal, with top-k off: every element falls
+    into one mass bin, and no key lies in a higher one (regression: the
+    search for a bin's key interval must end when nothing lies above)."""
+    rows, params = [], []
+    rows.append(np.zeros(V, np.float32)); params.append((0.7, 0, 0.5, 1.0, [], 0.37))
+    rows.append(np.zeros(V, np.float32)); params.append((1.3, 0, 1.0, 1.0, [], 0.91))
+    rows.append(np.full(V, -2.5, np.float32)); params.append((0.9, V, 0.9, 1.0, [], 0.05))
+    rows.append(np.ones(V, np.float32)); params.append((0.8, 0, 0.7, 1.2, [0, V // 2], 0.66))
+    T, k, p, pen, h, u = (list(c) for c in zip(*params))
+    w = custom("constant", np.stack(rows), T, k, p, pen, h, u)
+    say(f"[constant] V={V} rows={w.B}")
+    ref = run_oracle(oracle, w)
+    tok, st, probs = run_gpu(w, cuda)
+    check(w, ref, tok, st, probs)
