@@ -1006,10 +1006,15 @@ struct RowStream {
         ntile = (nvec + TV - 1) / TV;
         restart();
     }
+    // The first two tiles.  The tile numbers pass through an empty asm
+    // statement, so that the compiler computes these addresses at each use
+    // instead of keeping one set alive (in scratch) for all the passes.
     __device__ __forceinline__ void restart()
     {
-        load(A, 0);
-        load(Bf, 1);
+        int t0 = 0;
+        asm volatile("" : "+s"(t0));
+        load(A, t0);
+        load(Bf, t0 + 1);
     }
     // (no branch: a row with no whole vector reads a dummy vector instead)
     __device__ __forceinline__ void load(vec_t (&b)[FU], int t)
