@@ -761,12 +761,11 @@ struct Ranked {
 // Input, from the kernel's pass over the segments: every buffered element
 // with l >= l_est carries its bin + 1 in bits 18 and up of its id word
 // (V <= 2^18), the others 0 there; CH holds the counts per bin (2048 bins
-// linear in d = l - m on [l_est - m, 0], monotone in the sorted order), CS
-// the counts per group of 32 bins.
+// linear in d = l - m on [l_est - m, 0], monotone in the sorted order).
 //
-// Every wave finds the bin kb of the k-th largest by itself.  CH then turns
-// into the offsets of the bins in descending order (a counting sort), and a
-// second pass places the elements of the bins >= kb (they include the top-k
+// CH turns into the offsets of the bins in descending order (a counting
+// sort), which also names the bin kb of the k-th largest, and a second pass
+// places the elements of the bins >= kb (they include the top-k
 // set) there in the kept list KL, bin by bin, with their masses, which also
 // go into MH / MS.  After that pass CH[b] is the end of bin b in KL and
 // CH[b + 1] its start.  Wave 0 resolves the k-th, the top-p cut and the draw,
@@ -781,8 +780,8 @@ static_assert(KL_CAP * 16 <= KF_MH - KF_BM, "the kept list fits where the histor
 
 __device__ __forceinline__ bool finish_segs(const Params& p, int r, const uint32_t* ck, const uint32_t* ci,
                                             const uint32_t* seg, float T, bool neg, uint32_t kk, float m,
-                                            float top_p, float u, u64* MH, uint32_t* CH, u64* MS,
-                                            const uint32_t* CS, u64* KL, int64_t& tok, int32_t& st)
+                                            float top_p, float u, u64* MH, uint32_t* CH, u64* MS, u64* KL,
+                                            int64_t& tok, int32_t& st)
 {
     __shared__ int g_fail;
     __shared__ u64 g_tok, g_wk, g_cut;
@@ -794,13 +793,11 @@ __device__ __forceinline__ bool finish_segs(const Params& p, int r, const uint32
     const uint32_t* wck = ck + wv * FSEG;
     const uint32_t* wci = ci + wv * FSEG;
 
-    // the k-th's bin, by every wave; the size of KL
-    const WHit hk = wave_find_desc<uint32_t>(CH, (u64)CS[lane], (u64)(kk - 1u));
-    const int kb = hk.bin;
-    const uint32_t nkb = CH[kb];
-    if (hk.above + nkb > (u64)KL_CAP || nkb > 64u) return false;
-    // CH -> exclusive offsets in descending bin order: this thread's 4 bins
-    // are 2047 - 4 tid down to 2044 - 4 tid
+    // CH -> exclusive offsets in descending bin order (this thread's 4 bins
+    // are 2047 - 4 tid down to 2044 - 4 tid); the thread whose bins hold
+    // position k - 1 names the k-th's bin
+    __shared__ int g_kb;
+    __shared__ uint32_t g_kabove, g_kn;
     {
         uint32_t c[4], sum = 0;
 #pragma unroll
@@ -808,9 +805,18 @@ __device__ __forceinline__ bool finish_segs(const Params& p, int r, const uint32
         uint32_t total;
         uint32_t off = block_incl_scan<uint32_t>(sum, &total) - sum;   // (its barriers end the reads above)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) { CH[2047 - 4 * tid - i] = off; off += c[i]; }
+        for (int i = 0; i < 4; ++i) {
+            const int b = 2047 - 4 * tid - i;
+            if (off <= kk - 1u && kk - 1u < off + c[i]) { g_kb = b; g_kabove = off; g_kn = c[i]; }
+            CH[b] = off;
+            off += c[i];
+        }
     }
     __syncthreads();
+    // (at least k elements are binned: the bound held)
+    const int kb = g_kb;
+    const uint32_t nabove = g_kabove, nkb = g_kn;
+    if (nabove + nkb > (uint32_t)KL_CAP || nkb > 64u) return false;
     // the bins from kb up: masses, and their places in KL
     const uint32_t tkb = (uint32_t)kb + 1u;
     // four entries per lane at a time: loads, then arithmetic, then the
@@ -885,7 +891,7 @@ __device__ __forceinline__ bool finish_segs(const Params& p, int r, const uint32
         // sampling.py:52-54: the k-th largest of its bin; its value ties stay
         Ranked q = load_bin(kb);
         int qb = kb;
-        const uint32_t rk = (kk - 1u) - (uint32_t)hk.above;
+        const uint32_t rk = (kk - 1u) - nabove;
         const u64 mk = __ballot(q.valid && q.gt == rk);
         if (!mk) fail = true;
         const uint32_t vkk = (uint32_t)(readlane64(q.key, mk ? __builtin_ctzll(mk) : 0) >> 32);
@@ -1943,9 +1949,8 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
             bool thk_known = false;
             if (segs) {
                 if (binned) {
-                    group_sums<uint32_t>(hist, s_cs);
                     // (its kept list goes where the history bitmap was)
-                    done = finish_segs(p, r, ck, ci, s_seg, T, neg, kk, m0, top_p, u, MH, hist, s_ms, s_cs,
+                    done = finish_segs(p, r, ck, ci, s_seg, T, neg, kk, m0, top_p, u, MH, hist, s_ms,
                                        (u64*)(smem + KF_BM), tok, st);
                     if (!done && pen_on) {   // the general path needs the bitmap again
                         const int words = (V + 31) >> 5;
