@@ -710,10 +710,13 @@ struct WHit {
 // the bin b of h[0, 2048) with above(b) <= t < above(b) + h[b], where
 // above(b) is the sum of the bins above b.  Requires t < the total.
 template <typename T>
-__device__ __forceinline__ WHit wave_find_desc(const T* h, u64 s, u64 t)
+__device__ __forceinline__ WHit wave_find_desc(const T* h, u64 s, u64 t);
+
+// The same, with incl = wave_suffix_incl(s) computed once by the caller.
+template <typename T>
+__device__ __forceinline__ WHit wave_find_desc_pre(const T* h, u64 s, u64 incl, u64 t)
 {
     const int lane = lane_id();
-    const u64 incl = wave_suffix_incl(s);
     const u64 msk = __ballot(incl - s <= t && t < incl);
     const int L = msk ? __builtin_ctzll(msk) : 0;
     const u64 a = readlane64(incl - s, L);
@@ -723,6 +726,11 @@ __device__ __forceinline__ WHit wave_find_desc(const T* h, u64 s, u64 t)
     const u64 m2 = __ballot(lane < 32 && a + pi - v <= t && t < a + pi);
     const int j = m2 ? __builtin_ctzll(m2) : 0;
     return WHit{32 * L + 31 - j, a + readlane64(pi - v, j)};
+}
+template <typename T>
+__device__ __forceinline__ WHit wave_find_desc(const T* h, u64 s, u64 t)
+{
+    return wave_find_desc_pre<T>(h, s, wave_suffix_incl(s), t);
 }
 
 // Called by one whole wave: the sum of h over the bins above b.
@@ -861,6 +869,7 @@ __device__ __forceinline__ bool finish_segs(const Params& p, int r, const uint32
     if (wv == 0) {
         bool fail = false;
         const u64 ms = MS[lane];
+        const u64 msuf = wave_suffix_incl(ms);   // (for every search below)
         const u64 Ak = wave_sum_above<u64>(MH, ms, kb);
         // bin b's elements, one per lane, ranked
         auto load_bin = [&](int b) -> Ranked {
@@ -902,7 +911,7 @@ __device__ __forceinline__ bool finish_segs(const Params& p, int r, const uint32
             int b = kb;
             u64 A = Ak;
             if (x < Ak) {
-                const WHit h = wave_find_desc<u64>(MH, ms, x);
+                const WHit h = wave_find_desc_pre<u64>(MH, ms, msuf, x);
                 b = h.bin;
                 A = h.above;
             }
