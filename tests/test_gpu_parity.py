@@ -280,3 +280,15 @@ def test_parity_constant_rows_top_p_only(oracle, cuda, V):
     ref = run_oracle(oracle, w)
     tok, st, probs = run_gpu(w, cuda)
     check(w, ref, tok, st, probs)
+
+
+def test_parity_fp16_top_k_rows(oracle, cuda):
+    """fp16 rows through the top-k path (the fp16 workload itself has top-k
+    off): 128-bit loads of eight halves, converted in registers."""
+    w = make_workload("zipf", B=24)
+    w16 = Workload("zipf16", w.logits.astype(np.float16), w.temperature, w.top_k, w.top_p,
+                   w.penalty, w.hist_offsets, w.hist_ids, w.uniforms)
+    say(f"[fp16-topk] B={w16.B} V={w16.V}")
+    ref = run_oracle(oracle, w16)
+    tok, st, probs = run_gpu(w16, cuda)
+    check(w16, ref, tok, st, probs)
