@@ -1598,7 +1598,7 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
     auto build_bitmap = [&]() -> bool {
         bool bad = false;
         if (pen_on) {
-            const bool list = mode == MODE_LARGE;
+            const bool list = mode == MODE_LARGE || mode == MODE_GREEDY;
             auto add = [&](int id) {
                 if (id < 0 || id >= V) { bad = true; return; }
                 const uint32_t bit = 1u << (id & 31);
@@ -1621,15 +1621,99 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
     }
     if (st == MXS_ROW_OK && mode == MODE_INVALID) st = MXS_ROW_BAD_PARAM;
 
-    if (st == MXS_ROW_OK && mode == MODE_GREEDY) {   // sampling.py:47-48
-        uint32_t bk = 0, bi = 0;
-        rs.run_pen(bm, pen_on, pen,
+    // The penalized row's extremes from a raw stream (no penalty branch per
+    // element): key_of(x) ranks a value; best gets the packed maximum
+    // (key << 32 | ~index: the first index among equal keys), kmin the
+    // smallest key over the raw row and the penalized history values (a
+    // bound, and a witness of NaNs and infinities).  The history ids'
+    // penalized values are folded in from the deduplicated list.  Returns
+    // false when the raw maximum is itself a history id (the largest of the
+    // other elements is then unknown): the caller streams again with the
+    // penalty applied.  Requires the list (greedy and top-k-off rows) and a
+    // penalty in (0, inf).
+    const bool raw_ok = pen_on && pen > 0.0f && pen <= 3.402823466e38f &&
+                        (mode == MODE_GREEDY || mode == MODE_LARGE);
+    auto raw_extremes = [&](auto key_of, u64& best, uint32_t& kmin) -> bool {
+        __shared__ u64 s_rp[NWAVES], s_hp[NWAVES];
+        __shared__ uint32_t s_mn[NWAVES];
+        uint32_t bk = 0, bi = 0, mn = 0xFFFFFFFFu;
+        rs.template run<false>(bm, pen,
             [&](int, int e, float x) {
-                const uint32_t g = (x != x) ? 0xFFFFFFFFu : vkey(x);   // NaN is the maximum
-                if (g > bk) { bk = g; bi = (uint32_t)e; }              // ascending e: the first maximum
+                const uint32_t g = key_of(x);
+                if (g > bk) { bk = g; bi = (uint32_t)e; }   // ascending e: the first maximum
+                mn = g < mn ? g : mn;
             },
             [&](auto&&) { return false; });
-        const u64 best = block_max<u64>(bk ? (((u64)bk << 32) | (u64)(0xFFFFFFFFu - bi)) : 0ull);
+        u64 hp = 0;
+        const uint32_t nh = s_nh;
+        auto fold = [&](int id, float x0) {
+            const uint32_t g = key_of(penalize(x0, pen));
+            const u64 pk = ((u64)g << 32) | (u64)(0xFFFFFFFFu - (uint32_t)id);
+            hp = pk > hp ? pk : hp;
+            mn = g < mn ? g : mn;
+        };
+        if (nh <= (uint32_t)HCAP) {
+            for (uint32_t i0 = tid; i0 < nh; i0 += 4 * NT) {   // loads four at a time
+                int id[4];
+                float xv[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const uint32_t i = i0 + (uint32_t)(q * NT);
+                    id[q] = i < nh ? (int)hl[i] : -1;
+                }
+#pragma unroll
+                for (int q = 0; q < 4; ++q) xv[q] = VecIO<TIn>::one(rowp, id[q] >= 0 ? id[q] : 0);
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    if (id[q] >= 0) fold(id[q], xv[q]);
+            }
+        } else {
+            const int words = (V + 31) >> 5;
+            for (int wd = tid; wd < words; wd += NT) {
+                uint32_t bits = bm[wd];
+                while (bits) {
+                    const int bi2 = __builtin_ctz(bits);
+                    bits &= bits - 1u;
+                    fold(wd * 32 + bi2, VecIO<TIn>::one(rowp, wd * 32 + bi2));
+                }
+            }
+        }
+        const u64 rp = bk ? (((u64)bk << 32) | (u64)(0xFFFFFFFFu - bi)) : 0ull;
+        const u64 a0 = wave_max<u64>(rp), a1 = wave_max<u64>(hp);
+        const uint32_t a2 = wave_min_u32(mn);
+        if (lane == 0) { s_rp[wave_id()] = a0; s_hp[wave_id()] = a1; s_mn[wave_id()] = a2; }
+        __syncthreads();
+        u64 rb = 0, hb = 0;
+        kmin = 0xFFFFFFFFu;
+#pragma unroll
+        for (int v = 0; v < NWAVES; ++v) {
+            rb = s_rp[v] > rb ? s_rp[v] : rb;
+            hb = s_hp[v] > hb ? s_hp[v] : hb;
+            kmin = s_mn[v] < kmin ? s_mn[v] : kmin;
+        }
+        __syncthreads();   // (the arrays may be read again)
+        const uint32_t arg = 0xFFFFFFFFu - (uint32_t)rb;
+        if (rb && ((bm[arg >> 5] >> (arg & 31)) & 1u)) return false;
+        best = rb > hb ? rb : hb;
+        return true;
+    };
+
+    if (st == MXS_ROW_OK && mode == MODE_GREEDY) {   // sampling.py:47-48
+        auto gkey = [](float x) -> uint32_t { return (x != x) ? 0xFFFFFFFFu : vkey(x); };   // NaN is the maximum
+        u64 best = 0;
+        uint32_t kmin;
+        bool have = raw_ok && raw_extremes(gkey, best, kmin);
+        if (!have) {
+            if (raw_ok) rs.restart();
+            uint32_t bk = 0, bi = 0;
+            rs.run_pen(bm, pen_on, pen,
+                [&](int, int e, float x) {
+                    const uint32_t g = gkey(x);
+                    if (g > bk) { bk = g; bi = (uint32_t)e; }   // ascending e: the first maximum
+                },
+                [&](auto&&) { return false; });
+            best = block_max<u64>(bk ? (((u64)bk << 32) | (u64)(0xFFFFFFFFu - bi)) : 0ull);
+        }
         tok = (int64_t)(0xFFFFFFFFu - (uint32_t)best);
         if (p.out_probs && tid == 0) p.out_probs[(size_t)r * (size_t)V + (size_t)tok] = 1.0f;
     } else if (st == MXS_ROW_OK) {
@@ -1656,6 +1740,7 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
         uint32_t est = 0, cmax = 0;   // the sampled estimate; the buffer's largest penalized key
         bool segs = false;            // the candidates are in the stream's per-wave segments
         bool binned = false;          // ... and carry their bins, counts and final masses
+        bool have_rd = false;         // rd holds the penalized row's extremes
         float m0 = 0.0f, lest = 0.0f;
         Reduced rd{0u, 0xFFFFFFFFu, 0u};
         u64* MH = (u64*)(smem + KF_MH);
@@ -1935,15 +2020,23 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                 if (!overflow) fix_up();
             }
         } else {
-            rs.run_pen(bm, pen_on, pen,
-                [&](int, int, float x) {
-                    const uint32_t sk = selkey(x, neg);
-                    omax = sk > omax ? sk : omax;
-                    omin = sk < omin ? sk : omin;
-                },
-                [&](auto&&) { return false; });
+            u64 best = 0;
+            uint32_t kmin = 0;
+            if (raw_ok && raw_extremes([&](float x) { return selkey(x, neg); }, best, kmin)) {
+                rd = Reduced{(uint32_t)(best >> 32), kmin, 0u};
+                have_rd = true;
+            } else {
+                if (raw_ok) rs.restart();
+                rs.run_pen(bm, pen_on, pen,
+                    [&](int, int, float x) {
+                        const uint32_t sk = selkey(x, neg);
+                        omax = sk > omax ? sk : omax;
+                        omin = sk < omin ? sk : omin;
+                    },
+                    [&](auto&&) { return false; });
+            }
         }
-        if (!segs) rd = block_reduce(omax, omin, 0u);
+        if (!segs && !have_rd) rd = block_reduce(omax, omin, 0u);
         // NaN keys lie above the key of +inf and below that of -inf (the
         // reversed keys of T < 0 swap the two ranges)
         const bool has_nan = rd.max > 0xFF800000u || rd.min < 0x007FFFFFu;

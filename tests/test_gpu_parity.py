@@ -292,3 +292,32 @@ def test_parity_fp16_top_k_rows(oracle, cuda):
     ref = run_oracle(oracle, w16)
     tok, st, probs = run_gpu(w16, cuda)
     check(w16, ref, tok, st, probs)
+
+
+def test_parity_history_and_row_extremes(oracle, cuda):
+    """Greedy and top-k-off rows take the row's extremes from a raw pass and
+    fold in the penalized history afterwards; rows whose raw maximum is a
+    history id stream again with the penalty applied."""
+    V = VOCAB
+    rng = np.random.default_rng(11)
+    base = (2.0 * rng.standard_normal(V)).astype(np.float32)
+    top = [int(i) for i in np.argsort(-base, kind="stable")[:8]]
+    rows, params = [], []
+    #               T     k     p     pen   hist                       u
+    rows.append(base); params.append((0.0, 0, 1.0, 1.3, top[:1] + [5, 6], 0.0))     # greedy, max penalized
+    rows.append(base); params.append((0.0, 0, 1.0, 1.3, [5, 6, 7], 0.0))            # greedy, max not in history
+    rows.append(base); params.append((0.0, 0, 1.0, 0.5, [5, 6, 7], 0.0))            # greedy, penalty raises
+    rows.append(base); params.append((0.8, 0, 0.9, 1.3, top[:2], 0.3))             # top-p, max penalized
+    rows.append(base); params.append((0.8, 0, 0.9, 1.3, [9, 10, 11], 0.7))          # top-p, max not in history
+    rows.append(base); params.append((0.8, 0, 0.9, 0.6, list(range(0, V, 5)), 0.5))  # top-p, penalty raises
+    rows.append(base); params.append((-0.7, 0, 0.8, 1.2, top[:3] + [1], 0.4))      # top-p, T < 0
+    rows.append(base); params.append((0.9, 2000, 0.95, 1.1, top[:4], 0.8))         # k above the candidate cap
+    rn = base.copy(); rn[top[0]] = np.nan
+    rows.append(rn); params.append((0.8, 0, 0.9, 1.2, top[:1], 0.5))               # NaN among the history ids
+    rows.append(rn.copy()); params.append((0.0, 0, 1.0, 1.2, top[:1], 0.0))        # greedy, NaN in history
+    T, k, p, pen, h, u = (list(c) for c in zip(*params))
+    w = custom("extremes", np.stack(rows), T, k, p, pen, h, u)
+    say(f"[extremes] rows={w.B}")
+    ref = run_oracle(oracle, w)
+    tok, st, probs = run_gpu(w, cuda)
+    check(w, ref, tok, st, probs)
