@@ -86,6 +86,31 @@ __host__ __device__ __forceinline__ u64 mass_of(float d)
     return (u64)(P >> (-s));
 }
 
+// c * mass_of(d) for c < 2^16 and d <= 0 (0 for NaN), without branches: P (< 2^25)
+// is shifted right first when the exponent is negative, as mass_of does.
+__device__ __forceinline__ u64 count_mass(uint32_t c, float d)
+{
+    const float dc = __builtin_fminf(d, 0.0f);   // (d itself for d <= 0; keeps n finite)
+    const float t = dc * 0x1.715476p+0f;
+    const float n = __builtin_rintf(t);
+    float r = __builtin_fmaf(n, -0x1.62e4p-1f, dc);
+    r = __builtin_fmaf(n, -0x1.7f7d1cp-20f, r);
+    float q = 0x1.a01a02p-13f;
+    q = __builtin_fmaf(q, r, 0x1.6c16c2p-10f);
+    q = __builtin_fmaf(q, r, 0x1.111112p-7f);
+    q = __builtin_fmaf(q, r, 0x1.555556p-5f);
+    q = __builtin_fmaf(q, r, 0x1.555556p-3f);
+    q = __builtin_fmaf(q, r, 0.5f);
+    q = __builtin_fmaf(q, r, 1.0f);
+    q = __builtin_fmaf(q, r, 1.0f);
+    const uint32_t P = (uint32_t)(q * 16777216.0f);
+    const int s = MASS_SHIFT + (int)n;   // (n >= -152 where d >= -104)
+    const uint32_t ce = d >= -104.0f ? c : 0u;
+    const uint32_t Ps = s >= 0 ? P : P >> (-s < 31 ? -s : 31);
+    const uint32_t sh = s >= 0 ? (uint32_t)s : 0u;
+    return ((u64)ce * (u64)Ps) << sh;
+}
+
 // v in [0, 1) as M * 2^-sh, M < 2^24.
 __host__ __device__ __forceinline__ void split_unit(float v, uint32_t& M, int& sh)
 {

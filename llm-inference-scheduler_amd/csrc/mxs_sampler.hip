@@ -17,6 +17,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "mxs_device.h"
 #include "mxs_sampler.h"
 
@@ -1136,6 +1138,39 @@ struct RowStream {
         if (pen_inline) run<true>(bm, pen, elem, tile_end);
         else run<false>(bm, pen, elem, tile_end);
     }
+    // One pass over the raw 16-bit values of an fp16 row: vec(v, e) for each
+    // whole vector (elements e .. e + 7, two per 32-bit word), then
+    // one(bits16, e) for the elements after the last whole vector.
+    template <class Vec, class One>
+    __device__ __forceinline__ void run_raw(Vec&& vec, One&& one)
+    {
+        static_assert(VW == 8, "fp16 rows");
+        const int tid = threadIdx.x;
+        const int nfull = nvec / TV;
+        auto words = [&](const vec_t (&b)[FU], int t, bool part) {
+#pragma unroll
+            for (int j = 0; j < FU; ++j) {
+                const int vi = t * TV + j * NT + tid;
+                if (part && vi >= nvec) continue;
+                vec(b[j], vi * VW);
+            }
+        };
+        int t = 0;
+        for (; t + 1 < nfull; t += 2) {
+            words(A, t, false);
+            load(A, t + 2);
+            words(Bf, t + 1, false);
+            load(Bf, t + 3);
+        }
+        if (t < nfull) {
+            words(A, t, false);
+            ++t;
+#pragma unroll
+            for (int j = 0; j < FU; ++j) A[j] = Bf[j];
+        }
+        if (t < ntile) words(A, t, true);
+        for (int e = nvec * VW + tid; e < V; e += NT) one((uint32_t)__builtin_bit_cast(uint16_t, rowp[e]), e);
+    }
 };
 
 // One pass over a row from its first tile.
@@ -1491,6 +1526,501 @@ __device__ __forceinline__ bool finish_wide(const Params& p, int r, float T, boo
     return true;
 }
 
+// ---------------------------------------------------------------- fp16 rows, top-k off
+//
+// An fp16 logit is one of 65536 values, and for 2^-100 < |T| < 2^100 its
+// tempered value fl32(x / T) is a strictly monotone function of them:
+// neighbouring fp16 values differ by at least 2^-11 relative, far more than
+// the fp32 rounding of the quotient moves them, and no quotient leaves the
+// normal range.  -0 and +0 are the one pair with equal values.  So the
+// sorted order of sampling.py:56-57 (value desc, index asc) is the order of
+// the values' ranks R = 0, 1, ..., the elements of one rank in index order,
+// and one pass that counts each rank's elements (16-bit counters, two per
+// LDS word) gives every prefix mass: each rank's mass is its count times one
+// mass_of, computed once per value present.  The top-p cut and the draw
+// search the ranks' masses in chunks of 128 ranks; the only other pass over
+// the row marks the elements of the drawn rank to find the one at the drawn
+// position in index order.
+//
+// The penalized history ids (at most HCAP) leave their raw ranks and are
+// placed by their penalized values: an id whose value equals rank R's joins
+// R's tie group (same mass, index order), one strictly between the values of
+// R and R + 1 follows R's group.  Each thread keeps up to HQ of them in
+// registers.
+//
+// The counts overwrite the history bitmap and list, which are rebuilt when
+// a row falls back to the general path: a rank holding 65536 or more
+// elements, or more than GCAP history ids placed in one chunk.
+//
+// Ranks: R = h ^ KP for an fp16 pattern h >= 0, h ^ KN for h < 0, with
+// (KP, KN) = (0x7FFF, 0) for T > 0 and (0x8000, 0xFFFF) for T < 0.  R < 0x3FF
+// and R > 0xFC00 are NaN patterns, 0x3FF holds the value +inf and 0xFC00 the
+// value -inf; ranks 0x7FFF and 0x8000 both hold 0 and the counts of 0x8000
+// move to 0x7FFF after the pass.
+constexpr int KC_CS = 131072;               // 512 x u64: mass of each chunk of 128 ranks
+constexpr int KC_HS = KC_CS + 4096;         // 512 x u64: penalized history mass placed in each chunk
+constexpr int KC_G = KC_HS + 4096;          // the history ids placed in one chunk
+constexpr int GCAP = 256;
+constexpr int HQ = 4;
+constexpr uint32_t RK_PINF = 0x3FFu, RK_NINF = 0xFC00u, RK_ZERO = 0x7FFFu;
+constexpr int FC_MIN_V = 32768;             // shorter rows take the general path
+static_assert(KC_G + 20 * GCAP <= KF_LDS_BYTES, "chunk history list");
+static_assert(HCAP <= HQ * NT, "history ids held in registers");
+static_assert(MXS_MAX_VOCAB / 8 <= 32768, "two index bitmaps in the counts' area");
+
+// An element at a mass position of the sorted order.
+struct CPick {
+    u64 E;          // mass before it
+    u64 w;          // its mass
+    u64 i;          // a raw element: its position among rank R's tie group, in index order
+    uint32_t R;     // its rank (a history element: the rank it follows or ties)
+    uint32_t id;    // a history element: its id; else 0xFFFFFFFF
+    float l;        // its tempered value
+    uint32_t ok;
+};
+
+// a / b for a < 2^62 and 0 < b (a double estimate, corrected)
+__device__ __forceinline__ u64 udiv_est(u64 a, u64 b)
+{
+    u64 q = (u64)((double)a / (double)b);
+    while (q > 0 && q * b > a) --q;
+    while ((q + 1) * b <= a) ++q;
+    return q;
+}
+
+// Returns false (history bitmap and list restored, rs restarted) when the
+// row must take the general path.
+__device__ __forceinline__ bool finish_counts(const Params& p, int r, RowStream<__half>& rs, float T, bool neg,
+                                              float top_p, float u, float pen, bool pen_on, uint32_t* bm,
+                                              uint32_t* hl, uint32_t nh, unsigned char* smem,
+                                              int64_t& tok, int32_t& st)
+{
+    __shared__ uint32_t s_csum, s_flag, s_ng, s_own, s_rtop, s_nb;
+    __shared__ u64 s_ownE;
+    __shared__ CPick s_pick;
+    const int tid = threadIdx.x, lane = lane_id();
+    const int V = p.V;
+    const __half* rowp = (const __half*)p.logits + (size_t)r * (size_t)p.ld;
+    uint32_t* cnt = (uint32_t*)smem;
+    u64* CS = (u64*)(smem + KC_CS);
+    u64* HS = (u64*)(smem + KC_HS);
+    uint32_t* GR = (uint32_t*)(smem + KC_G);
+    float* GL = (float*)(smem + KC_G + 4 * GCAP);
+    uint32_t* GI = (uint32_t*)(smem + KC_G + 8 * GCAP);
+    u64* GW = (u64*)(smem + KC_G + 12 * GCAP);
+    const uint32_t KP = neg ? 0x8000u : 0x7FFFu, KN = neg ? 0xFFFFu : 0u;
+    const uint32_t KPAIR = KP * 0x10001u;
+    const uint32_t XA = neg ? 0xFFFFu : 0x7FFFu, XB = neg ? 0x8000u : 0u;   // inverse: h = R ^ (R < 0x8000 ? XA : XB)
+    constexpr uint32_t OVF = 1u, NANB = 2u;
+    auto rank_of = [&](uint32_t h) { return h ^ ((h & 0x8000u) ? KN : KP); };
+    auto count_of = [&](uint32_t R) { return (cnt[R >> 1] >> ((R & 1u) << 4)) & 0xFFFFu; };
+    auto inc_of = [](uint32_t R) { return 1u + (R & 1u) * 0xFFFFu; };
+    auto val_fin = [&](uint32_t R) { return VecIO<__half>::h2f(R ^ (R < 0x8000u ? XA : XB)) / T; };
+    auto val_of = [&](uint32_t R) -> float {   // monotone over all ranks (NaN ranks: +-inf)
+        const float v = val_fin(R);
+        return R < RK_PINF ? INFINITY : (R > RK_NINF ? -INFINITY : v);
+    };
+
+    // the history ids, HQ per thread, and their raw values
+    int hid[HQ];
+    float hx[HQ];
+#pragma unroll
+    for (int q = 0; q < HQ; ++q) {
+        const uint32_t i = (uint32_t)(tid + q * NT);
+        hid[q] = (pen_on && i < nh) ? (int)hl[i] : -1;
+    }
+#pragma unroll
+    for (int q = 0; q < HQ; ++q) hx[q] = VecIO<__half>::one(rowp, hid[q] >= 0 ? hid[q] : 0);
+    const uint32_t nhe = pen_on ? nh : 0u;
+    auto restore = [&]() {   // the general path's history bitmap and list
+        __syncthreads();
+        if (pen_on) {
+            const int words = (V + 31) >> 5;
+            for (int w = tid; w < words; w += NT) bm[w] = 0;
+            __syncthreads();
+#pragma unroll
+            for (int q = 0; q < HQ; ++q)
+                if (hid[q] >= 0) {
+                    atomicOr(&bm[hid[q] >> 5], 1u << (hid[q] & 31));
+                    hl[tid + q * NT] = (uint32_t)hid[q];
+                }
+        }
+        __syncthreads();
+        rs.restart();
+    };
+    __syncthreads();   // (the list lies in the counts' area)
+    {
+        uint4* c4 = (uint4*)smem;
+#pragma unroll
+        for (int i = 0; i < KC_CS / 16 / NT; ++i) c4[tid + i * NT] = uint4{0u, 0u, 0u, 0u};
+        HS[tid] = 0;
+        if (tid == 0) { s_csum = 0; s_flag = 0; s_ng = 0; s_own = 0xFFFFFFFFu; }
+    }
+    __syncthreads();
+
+    // sampling.py:56: the row's values, counted by rank
+    auto ranks2 = [&](uint32_t wd) {   // the ranks of a word's two values, in its two halves
+        const uint32_t s = (wd >> 15) & 0x00010001u;
+        return wd ^ (((s << 15) - s) ^ KPAIR);
+    };
+    uint32_t rmin = 0xFFFFu;
+    rs.run_raw(
+        [&](const RowStream<__half>::vec_t& v, int) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t Rp = ranks2(v[k]);
+                const uint32_t r0 = Rp & 0xFFFFu, r1 = Rp >> 16;
+                rmin = min(rmin, min(r0, r1));
+                atomicAdd(&cnt[r0 >> 1], inc_of(r0));
+                atomicAdd(&cnt[r1 >> 1], inc_of(r1));
+            }
+        },
+        [&](uint32_t h, int) {
+            const uint32_t R = rank_of(h);
+            rmin = R < rmin ? R : rmin;
+            atomicAdd(&cnt[R >> 1], inc_of(R));
+        });
+    // the history ids leave their raw ranks (sampling.py:38-45 penalizes them)
+    uint32_t hraw[HQ], hR[HQ];
+    float hv[HQ];
+    uint32_t hkey = 0, hnan = 0;
+#pragma unroll
+    for (int q = 0; q < HQ; ++q) {
+        hraw[q] = rank_of((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hx[q]));
+        hv[q] = penalize(hx[q], pen) / T;
+        if (hid[q] >= 0) {
+            atomicSub(&cnt[hraw[q] >> 1], inc_of(hraw[q]));
+            if (hv[q] != hv[q]) hnan = 1u;
+            else hkey = max(hkey, okey(hv[q]) + 1u);   // 0: none
+        }
+    }
+    const Reduced rd = block_reduce(hkey, rmin, hnan);   // (its barriers publish the counts)
+    if (tid == 0) {   // -0 joins +0
+        const uint32_t z = cnt[0x8000u >> 1] & 0xFFFFu;
+        const uint32_t t0 = (cnt[RK_ZERO >> 1] >> 16) + z;
+        if (t0 > 0xFFFFu) s_flag = OVF;
+        cnt[RK_ZERO >> 1] = (cnt[RK_ZERO >> 1] & 0xFFFFu) | (t0 << 16);
+        cnt[0x8000u >> 1] &= 0xFFFF0000u;
+    }
+    // a NaN, or +inf at the top (sampling.py:57-58)
+    if (rd.any || rd.min <= RK_PINF) { st = MXS_ROW_NONFINITE; tok = -1; return true; }
+    __syncthreads();
+    // the row's maximum: the first rank still holding elements, or a history value
+    uint32_t rtop = rd.min == 0x8000u ? RK_ZERO : rd.min;
+    if (count_of(rtop) == 0u) {
+        if (wave_id() == 0) {
+            uint32_t found = 0xFFFFFFFFu;
+            for (uint32_t base = (rtop + 1u) & ~127u; base < 65536u && found == 0xFFFFFFFFu; base += 128u) {
+                const uint32_t R0 = base + 2u * (uint32_t)lane;
+                const uint32_t wd = cnt[R0 >> 1];
+                const uint32_t c0 = R0 > rtop ? (wd & 0xFFFFu) : 0u, c1 = R0 + 1u > rtop ? (wd >> 16) : 0u;
+                const u64 m0 = __ballot(c0 != 0u), m1 = __ballot(c1 != 0u);
+                if (m0 | m1) {
+                    const int l0 = m0 ? __builtin_ctzll(m0) : 64, l1 = m1 ? __builtin_ctzll(m1) : 64;
+                    found = l0 <= l1 ? base + 2u * (uint32_t)l0 : base + 2u * (uint32_t)l1 + 1u;
+                }
+            }
+            if (lane == 0) s_rtop = found;
+        }
+        __syncthreads();
+        rtop = s_rtop;
+    }
+    float m = rtop != 0xFFFFFFFFu ? val_of(rtop) : -INFINITY;
+    if (rd.max) {
+        const float mh = okey_inv(rd.max - 1u);
+        m = mh > m ? mh : m;
+    }
+    if (!__builtin_isfinite(m)) { st = MXS_ROW_NONFINITE; tok = -1; return true; }
+
+    // each history value's place: the last rank whose value is >= it, from
+    // the rank of fp16(l * T) (the place itself or a neighbour)
+    {
+        float va[HQ], vb[HQ];
+#pragma unroll
+        for (int q = 0; q < HQ; ++q) {
+            hR[q] = rank_of((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(hv[q] * T)));
+            va[q] = val_of(hR[q]);
+            vb[q] = hR[q] < 0xFFFFu ? val_of(hR[q] + 1u) : -INFINITY;
+        }
+#pragma unroll
+        for (int q = 0; q < HQ; ++q) {
+            uint32_t R = hR[q];
+            const float l = hv[q];
+            if (hid[q] >= 0 && !(va[q] >= l && !(vb[q] >= l))) {
+                while (R > 0u && val_of(R) < l) --R;
+                while (R < 0xFFFFu && val_of(R + 1u) >= l) ++R;
+            }
+            hR[q] = R == 0x8000u ? RK_ZERO : R;
+        }
+    }
+
+    // sampling.py:57-58: the masses, per chunk of 128 ranks
+    {
+        uint32_t csum = 0, nanb = 0;
+        for (int c = wave_id(); c < 512; c += NWAVES) {
+            const uint32_t wd = cnt[64 * c + lane];
+            u64 acc = 0;
+            if (__ballot(wd != 0u)) {
+                const uint32_t R0 = 128u * (uint32_t)c + 2u * (uint32_t)lane;
+                const uint32_t c0 = wd & 0xFFFFu, c1 = wd >> 16;
+                acc = count_mass(c0, val_fin(R0) - m) + count_mass(c1, val_fin(R0 + 1u) - m);
+                csum += c0 + c1;
+                nanb |= ((R0 > RK_NINF && c0) || (R0 + 1u > RK_NINF && c1)) ? 1u : 0u;
+                acc = wave_sum<u64>(acc);
+            }
+            if (lane == 0) CS[c] = acc;
+        }
+        csum = wave_sum_u32(csum);
+        if (lane == 0) atomicAdd(&s_csum, csum);
+        if (__ballot(nanb != 0u) && lane == 0) atomicOr(&s_flag, NANB);
+#pragma unroll
+        for (int q = 0; q < HQ; ++q)
+            if (hid[q] >= 0) atomicAdd(&HS[hR[q] >> 7], mass_of(hv[q] - m));
+    }
+    __syncthreads();
+    if (s_csum != (uint32_t)V - nhe || (s_flag & OVF)) { restore(); return false; }
+    if (s_flag & NANB) { st = MXS_ROW_NONFINITE; tok = -1; return true; }
+    const u64 S = CS[tid] + HS[tid];
+    u64 W;
+    const u64 E0 = block_incl_scan<u64>(S, &W) - S;
+
+    // The element at mass position t < W.
+    auto pick = [&](u64 t) -> CPick {
+        if (E0 <= t && t - E0 < S) { s_own = (uint32_t)tid; s_ownE = E0; }
+        if (tid == 0) { s_ng = 0; s_pick.ok = 0; }
+        __syncthreads();
+        const uint32_t c = s_own;
+        const u64 Ec = s_ownE;
+        if (c < 512u) {
+#pragma unroll
+            for (int q = 0; q < HQ; ++q)
+                if (hid[q] >= 0 && (hR[q] >> 7) == c) {
+                    const uint32_t g = atomicAdd(&s_ng, 1u);
+                    if (g < (uint32_t)GCAP) {
+                        GR[g] = hR[q]; GL[g] = hv[q]; GI[g] = (uint32_t)hid[q]; GW[g] = mass_of(hv[q] - m);
+                    }
+                }
+        }
+        __syncthreads();
+        const uint32_t ng = s_ng;
+        if (tid == 0) s_own = 0xFFFFFFFFu;
+        if (c < 512u && ng <= (uint32_t)GCAP && wave_id() == 0) {
+            const u64 tr = t - Ec;
+            const uint32_t R0 = 128u * c + 2u * (uint32_t)lane;
+            const uint32_t wd = cnt[R0 >> 1];
+            const float l0 = val_of(R0), l1 = val_of(R0 + 1u);
+            const u64 w0 = mass_of(l0 - m), w1 = mass_of(l1 - m);
+            u64 M0 = (u64)(wd & 0xFFFFu) * w0, M1 = (u64)(wd >> 16) * w1;
+            uint32_t n0 = wd & 0xFFFFu, n1 = wd >> 16;   // tie groups
+            for (uint32_t g = 0; g < ng; ++g) {
+                const uint32_t gr = GR[g];
+                if (gr == R0) { M0 += GW[g]; n0 += GL[g] == l0 ? 1u : 0u; }
+                if (gr == R0 + 1u) { M1 += GW[g]; n1 += GL[g] == l1 ? 1u : 0u; }
+            }
+            const u64 incl = wave_prefix_u64(M0 + M1);
+            const u64 P = incl - (M0 + M1);
+            const bool here = P <= tr && tr < incl;
+            const u64 hm = __ballot(here);
+            if (hm) {
+                const int fl = __builtin_ctzll(hm);
+                u64 t2 = tr - P;
+                const bool second = t2 >= M0;
+                t2 -= second ? M0 : 0ull;
+                const uint32_t R = second ? R0 + 1u : R0;
+                const float lR = second ? l1 : l0;
+                const u64 wR = second ? w1 : w0;
+                const u64 tie = (u64)(second ? n1 : n0) * wR;
+                const uint32_t Rs = (uint32_t)__builtin_amdgcn_readlane((int)R, fl);
+                const float ls = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lR), fl));
+                const bool in_tie = __builtin_amdgcn_readlane(t2 < tie ? 1 : 0, fl) != 0;
+                if (in_tie) {
+                    if (here) {
+                        const u64 i = udiv_est(t2, wR);
+                        s_pick = CPick{t - (t2 - i * wR), wR, i, R, 0xFFFFFFFFu, lR, 1u};
+                    }
+                } else {
+                    // a penalized history value strictly between ranks Rs and Rs + 1:
+                    // those there in order of (value desc, index asc)
+                    const u64 tb = readlane64(t2 - tie, fl);
+                    for (uint32_t g0 = 0; g0 < ng; g0 += 64u) {
+                        const uint32_t g = g0 + (uint32_t)lane;
+                        if (g < ng && GR[g] == Rs && GL[g] < ls) {
+                            const u64 key = ((u64)vkey(GL[g]) << 32) | (u64)(0xFFFFFFFFu - GI[g]);
+                            u64 Eh = 0;
+                            for (uint32_t g2 = 0; g2 < ng; ++g2) {
+                                const u64 k2 = ((u64)vkey(GL[g2]) << 32) | (u64)(0xFFFFFFFFu - GI[g2]);
+                                if (GR[g2] == Rs && GL[g2] < ls && k2 > key) Eh += GW[g2];
+                            }
+                            if (Eh <= tb && tb - Eh < GW[g])
+                                s_pick = CPick{t - (tb - Eh), GW[g], 0ull, Rs, GI[g], GL[g], 1u};
+                        }
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        const CPick res = s_pick;
+        __syncthreads();
+        return res;
+    };
+
+    bool bounded = false;
+    CPick cut{0, 0, 0, 0, 0xFFFFFFFFu, 0.0f, 1u};
+    u64 Wk = W;
+    if (top_p < 1.0f) {   // sampling.py:56-63
+        if (!(top_p > 0.0f)) { st = MXS_ROW_EMPTY_NUCLEUS; tok = -1; return true; }
+        cut = pick(ceil_mul(top_p, W) - 1);
+        if (!cut.ok) { restore(); return false; }
+        bounded = true;
+        Wk = cut.E + cut.w;
+    }
+    const u64 D = floor_mul(clamp_uniform(u), Wk);   // sampling.py:69
+    const CPick dp = pick(D);
+    if (!dp.ok) { restore(); return false; }
+
+    // the index of a raw element: the i-th marked one of its rank
+    uint32_t tid_d = dp.id, tid_c = cut.id;
+    const bool need_d = dp.id == 0xFFFFFFFFu;
+    const bool need_c = p.out_probs && bounded && cut.id == 0xFFFFFFFFu;
+    if (need_d || need_c) {
+        rs.restart();
+        uint32_t* Bd = (uint32_t*)smem;
+        uint32_t* Bc = (uint32_t*)(smem + 32768);
+        const int words = (V + 31) >> 5;
+        for (int w = tid; w < words; w += NT) { Bd[w] = 0; Bc[w] = 0; }
+        __syncthreads();
+        const uint32_t Rd = need_d ? dp.R : 0xFFFFFFFFu, Rc = need_c ? cut.R : 0xFFFFFFFFu;
+        const uint32_t zd = Rd == RK_ZERO ? 1u : 0u, zc = Rc == RK_ZERO ? 1u : 0u;   // (rank 0x8000 is 0 too)
+        // the bits of a vector's eight elements, one LDS atomic per bitmap
+        // when any is set (elements e .. e + 7 share one bitmap word)
+        auto marks = [&](auto both) {
+            rs.run_raw(
+                [&](const RowStream<__half>::vec_t& v, int e) {
+                    uint32_t md = 0, mc = 0;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const uint32_t Rp = ranks2(v[k]);
+                        md |= ((Rp & 0xFFFFu) - Rd <= zd ? 1u : 0u) << (2 * k);
+                        md |= ((Rp >> 16) - Rd <= zd ? 2u : 0u) << (2 * k);
+                        if constexpr (decltype(both)::value) {
+                            mc |= ((Rp & 0xFFFFu) - Rc <= zc ? 1u : 0u) << (2 * k);
+                            mc |= ((Rp >> 16) - Rc <= zc ? 2u : 0u) << (2 * k);
+                        }
+                    }
+                    if (md) atomicOr(&Bd[e >> 5], md << (e & 31));
+                    if (mc) atomicOr(&Bc[e >> 5], mc << (e & 31));
+                },
+                [&](uint32_t h, int e) {
+                    const uint32_t R = rank_of(h);
+                    if (R - Rd <= zd) atomicOr(&Bd[e >> 5], 1u << (e & 31));
+                    if (R - Rc <= zc) atomicOr(&Bc[e >> 5], 1u << (e & 31));
+                });
+        };
+        if (need_c) marks(std::true_type{});
+        else marks(std::false_type{});
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < HQ; ++q)   // history ids are not in their raw ranks' groups ...
+            if (hid[q] >= 0) {
+                const uint32_t bit = 1u << (hid[q] & 31);
+                if (hraw[q] - Rd <= zd) atomicAnd(&Bd[hid[q] >> 5], ~bit);
+                if (hraw[q] - Rc <= zc) atomicAnd(&Bc[hid[q] >> 5], ~bit);
+            }
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < HQ; ++q)   // ... but in the group whose value they equal
+            if (hid[q] >= 0) {
+                const uint32_t bit = 1u << (hid[q] & 31);
+                if (hR[q] == Rd && hv[q] == dp.l) atomicOr(&Bd[hid[q] >> 5], bit);
+                if (hR[q] == Rc && hv[q] == cut.l) atomicOr(&Bc[hid[q] >> 5], bit);
+            }
+        __syncthreads();
+        auto nth_bit = [&](const uint32_t* B, u64 i) -> uint32_t {
+            const int per = (words + NT - 1) / NT;
+            const int w0 = tid * per;
+            uint32_t c = 0;
+            for (int k = 0; k < per; ++k)
+                if (w0 + k < words) c += (uint32_t)__builtin_popcount(B[w0 + k]);
+            if (tid == 0) s_nb = 0xFFFFFFFFu;
+            uint32_t tot;
+            const uint32_t incl = block_incl_scan<uint32_t>(c, &tot);
+            u64 before = incl - c;
+            if (before <= i && i < (u64)incl) {
+                for (int k = 0; k < per; ++k) {
+                    uint32_t b = B[w0 + k];
+                    const uint32_t pc = (uint32_t)__builtin_popcount(b);
+                    if (i < before + pc) {
+                        for (u64 j = before; j < i; ++j) b &= b - 1u;
+                        s_nb = (uint32_t)(32 * (w0 + k) + __builtin_ctz(b));
+                        break;
+                    }
+                    before += pc;
+                }
+            }
+            __syncthreads();
+            const uint32_t res = s_nb;
+            __syncthreads();
+            return res;
+        };
+        if (need_d) tid_d = nth_bit(Bd, dp.i);
+        if (need_c) tid_c = nth_bit(Bc, cut.i);
+        if (tid_d >= (uint32_t)V || (need_c && tid_c >= (uint32_t)V)) { restore(); return false; }
+    }
+    tok = (int64_t)tid_d;
+    st = MXS_ROW_OK;
+    if (p.out_probs) {   // sampling.py:68
+        __syncthreads();
+        if (pen_on) {   // the history bitmap again (its area held the counts)
+            const int words = (V + 31) >> 5;
+            for (int w = tid; w < words; w += NT) bm[w] = 0;
+            __syncthreads();
+#pragma unroll
+            for (int q = 0; q < HQ; ++q)
+                if (hid[q] >= 0) atomicOr(&bm[hid[q] >> 5], 1u << (hid[q] & 31));
+            __syncthreads();
+        }
+        const u64 bound = ((u64)vkey(cut.l) << 32) | (u64)(0xFFFFFFFFu - tid_c);
+        float* out = p.out_probs + (size_t)r * (size_t)V;
+        stream_row_pen<__half>(rowp, V, bm, pen_on, pen,
+            [&](int, int e, float x) {
+                const float l = x / T;
+                const u64 key = ((u64)vkey(l) << 32) | (u64)(0xFFFFFFFFu - (uint32_t)e);
+                if (!bounded || key >= bound) out[e] = (float)((double)mass_of(l - m) / (double)Wk);
+            },
+            [&](auto&&) { return false; });
+    }
+    return true;
+}
+
+// Rows that finish_counts serves: fp16, top-k off, long, a temperature
+// that keeps every tempered value distinct and normal, and a finite positive
+// penalty whose history fits the list.
+template <typename TIn>
+__device__ __forceinline__ bool counted_row(const Params& p, RowMode mode, int k, float T, float pen, bool pen_on,
+                                            uint32_t nh)
+{
+    if constexpr (sizeof(TIn) != 2) {
+        return false;
+    } else {
+        const float aT = __builtin_fabsf(T);
+        return mode == MODE_LARGE && (k <= 0 || k >= p.V) && p.V >= FC_MIN_V && aT > 0x1p-100f && aT < 0x1p100f &&
+               (!pen_on || (pen > 0.0f && pen <= 3.402823466e38f && nh <= (uint32_t)HCAP));
+    }
+}
+
+template <typename TIn>
+__device__ __forceinline__ bool finish_counts_as(const Params& p, int r, RowStream<TIn>& rs, float T, bool neg,
+                                                 float top_p, float u, float pen, bool pen_on, uint32_t* bm,
+                                                 uint32_t* hl, uint32_t nh, unsigned char* smem, int64_t& tok,
+                                                 int32_t& st)
+{
+    if constexpr (sizeof(TIn) != 2) {
+        return false;
+    } else {
+        return finish_counts(p, r, rs, T, neg, top_p, u, pen, pen_on, bm, hl, nh, smem, tok, st);
+    }
+}
+
 template <typename TIn>
 __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
 {
@@ -1599,19 +2129,35 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
         bool bad = false;
         if (pen_on) {
             const bool list = mode == MODE_LARGE || mode == MODE_GREEDY;
-            auto add = [&](int id) {
-                if (id < 0 || id >= V) { bad = true; return; }
-                const uint32_t bit = 1u << (id & 31);
-                const uint32_t old = atomicOr(&bm[id >> 5], bit);
-                if (list && !(old & bit)) {
-                    const uint32_t slot = atomicAdd(&s_nh, 1u);
-                    if (slot < (uint32_t)HCAP) hl[slot] = (uint32_t)id;
+            // (called by whole waves: the ids new to the bitmap take list
+            // slots with one atomic per wave)
+            auto add = [&](int id, bool valid) {
+                bool fresh = false;
+                if (valid) {
+                    if (id < 0 || id >= V) {
+                        bad = true;
+                    } else {
+                        const uint32_t bit = 1u << (id & 31);
+                        fresh = !(atomicOr(&bm[id >> 5], bit) & bit);
+                    }
+                }
+                if (list) {
+                    const u64 fm = __ballot(fresh);
+                    if (fm) {
+                        const int first = __builtin_ctzll(fm);
+                        uint32_t base = 0;
+                        if (lane == first) base = atomicAdd(&s_nh, (uint32_t)__builtin_popcountll(fm));
+                        const uint32_t slot = (uint32_t)__builtin_amdgcn_readlane((int)base, first) + lanes_below(fm);
+                        if (fresh && slot < (uint32_t)HCAP) hl[slot] = (uint32_t)id;
+                    }
                 }
             };
 #pragma unroll
-            for (int q = 0; q < HB; ++q)
-                if (h0 + tid + q * NT < h1) add(hv[q]);
-            for (int h = h0 + tid + HB * NT; h < h1; h += NT) add(p.hids[h]);
+            for (int q = 0; q < HB; ++q) add(hv[q], h0 + tid + q * NT < h1);
+            for (int hb = h0 + HB * NT; hb < h1; hb += NT) {
+                const int h = hb + tid;
+                add(h < h1 ? p.hids[h] : 0, h < h1);
+            }
         }
         return bad;
     };
@@ -1716,6 +2262,9 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
         }
         tok = (int64_t)(0xFFFFFFFFu - (uint32_t)best);
         if (p.out_probs && tid == 0) p.out_probs[(size_t)r * (size_t)V + (size_t)tok] = 1.0f;
+    } else if (st == MXS_ROW_OK && counted_row<TIn>(p, mode, k, T, pen, pen_on, s_nh) &&
+               finish_counts_as<TIn>(p, r, rs, T, neg, top_p, u, pen, pen_on, bm, hl, s_nh, smem, tok, st)) {
+        // an fp16 row with top-k off, finished from its value counts
     } else if (st == MXS_ROW_OK) {
         // selection keys of the penalized row: extremes (NaN and infinity
         // tests, the row maximum) and, for top-k rows, the candidates

@@ -321,3 +321,105 @@ def test_parity_history_and_row_extremes(oracle, cuda):
     ref = run_oracle(oracle, w)
     tok, st, probs = run_gpu(w, cuda)
     check(w, ref, tok, st, probs)
+
+
+def _counted_rows(V, seed=23):
+    """fp16 rows with top-k off, long enough for the value-count path, and
+    the cases its ranks and history placement have to get right."""
+    rng = np.random.default_rng(seed)
+    f16 = lambda a: np.asarray(a, dtype=np.float16)
+    base = f16(rng.standard_normal(V))
+    top = [int(i) for i in np.argsort(-base.astype(np.float32), kind="stable")[:16]]
+    hist2k = [int(i) for i in rng.choice(V, 2048, replace=False)]
+    rows, params = [], []
+    #                    T     k  p      pen   hist         u
+    rows.append(base); params.append((0.7, 0, 0.95, 1.05, hist2k, 0.37))        # the fp16 workload's row
+    rows.append(base); params.append((0.7, 0, 0.95, 1.05, hist2k, 0.0))
+    rows.append(base); params.append((0.7, 0, 0.95, 1.05, hist2k, 0.99999994))
+    rows.append(base); params.append((0.7, V, 1.0, 1.0, [], 0.61))             # k >= V, no cut, no history
+    rows.append(base); params.append((-0.8, 0, 0.9, 1.2, top[:3] + [1], 0.4))  # T < 0
+    rows.append(base); params.append((1.3, 0, 0.5, 0.7, top[:8] + hist2k[:500], 0.8))  # penalty raises values
+    rows.append(base); params.append((0.9, 0, 0.8, 1.3, top[:1], 0.05))        # the maximum is a history id
+    rows.append(base); params.append((0.9, 0, 0.8, 1.3, top[:16], 0.02))       # ... and the next fifteen
+    rows.append(base); params.append((0.9, 0, 1e-6, 1.1, hist2k[:64], 0.9))    # the cut at the first element
+    # penalized history values equal to raw values (pen 2: 2.0 -> 1.0): the
+    # tie groups interleave history and raw ids by index
+    tie = f16(rng.standard_normal(V) - 4.0)
+    ones = rng.choice(V, 300, replace=False)
+    twos = rng.choice(np.setdiff1d(np.arange(V), ones), 200, replace=False)
+    tie[ones] = 1.0
+    tie[twos] = 2.0
+    for u in (0.1, 0.5, 0.93):
+        rows.append(tie); params.append((1.0, 0, 1.0, 2.0, [int(i) for i in twos], u))
+    rows.append(tie); params.append((1.0, 0, 0.6, 2.0, [int(i) for i in twos[:150]], 0.7))
+    # penalized history values strictly between ranks: fifty equal ones on top
+    btw = f16(rng.standard_normal(V) - 3.0)
+    hb = rng.choice(V, 50, replace=False)
+    btw[hb] = 5.0
+    for u in (0.0, 0.45, 0.999):
+        rows.append(btw); params.append((0.8, 0, 1.0, 1.3, [int(i) for i in hb], u))
+    # more than 256 history ids placed in one chunk: the general path
+    many = f16(rng.standard_normal(V) - 3.0)
+    hm = rng.choice(V, 300, replace=False)
+    many[hm] = 5.0
+    rows.append(many); params.append((0.8, 0, 0.9, 1.3, [int(i) for i in hm], 0.3))
+    # heavy ties: four levels
+    lv = f16(rng.integers(0, 4, V) * 0.5)
+    rows.append(lv); params.append((0.5, 0, 0.7, 1.1, hist2k[:100], 0.66))
+    # +0 and -0 on top, mixed signs in index order
+    z = f16(np.full(V, -12.0))
+    zi = rng.choice(V, 400, replace=False)
+    z[zi] = np.where(rng.random(400) < 0.5, 0.0, -0.0)
+    for u in (0.2, 0.8):
+        rows.append(z); params.append((1.0, 0, 1.0, 1.0, [], u))
+    rows.append(z); params.append((-1.0, 0, 0.5, 1.5, [int(i) for i in zi[:10]], 0.4))
+    # masked rows: -inf below, and a rank holding 65536 or more elements
+    msk = base.copy()
+    msk[rng.choice(V, V // 3, replace=False)] = -np.inf
+    rows.append(msk); params.append((0.7, 0, 0.95, 1.05, hist2k, 0.5))
+    msk2 = base.copy()
+    msk2[: 70000] = -np.inf
+    rows.append(msk2); params.append((0.7, 0, 0.95, 1.05, hist2k, 0.5))
+    big = base.copy()
+    big[rng.choice(V, 70000, replace=False)] = 0.25
+    rows.append(big); params.append((0.7, 0, 0.9, 1.0, [], 0.5))
+    # non-finite rows
+    for bits in (0x7E00, 0xFE00, 0x7C00):   # NaN, NaN with the sign bit, +inf
+        b = base.copy(); b.view(np.uint16)[V // 2] = bits
+        rows.append(b); params.append((0.7, 0, 0.9, 1.05, hist2k[:10], 0.5))
+    b = base.copy(); b[V // 3] = -np.inf
+    rows.append(b); params.append((-0.7, 0, 0.9, 1.05, hist2k[:10], 0.5))        # -inf / T, T < 0: +inf
+    b = base.copy(); b[V // 3] = -np.inf
+    rows.append(b); params.append((0.7, 0, 0.0, 1.0, [], 0.5))                 # an empty nucleus
+    return rows, params
+
+
+def test_parity_fp16_value_counts(oracle, cuda):
+    """fp16 rows with top-k off finish from per-value counts: ranks, the
+    penalized history placed between or tied with them, the drawn element's
+    index found by a second pass; and the rows that fall back."""
+    V = VOCAB
+    rows, params = _counted_rows(V)
+    T, k, p, pen, h, u = (list(c) for c in zip(*params))
+    w = custom("counts16", np.stack(rows), T, k, p, pen, h, u)
+    say(f"[counts16] rows={w.B} V={V}")
+    ref = run_oracle(oracle, w)
+    tok, st, probs = run_gpu(w, cuda)
+    check(w, ref, tok, st, probs)
+    say("[counts16] no probabilities")
+    tok2, st2, _ = run_gpu(w, cuda, probs=False)
+    check(w, ref, tok2, st2, None)
+
+
+def test_parity_fp16_value_counts_unaligned(oracle, cuda):
+    """Odd row lengths: every other row is not 16-byte aligned and is
+    counted element by element."""
+    V = 40001
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((3, V)).astype(np.float16)
+    hists = [[int(i) for i in rng.choice(V, 300, replace=False)] for _ in range(3)]
+    w = custom("counts16-odd", x, [0.7, -0.9, 1.1], 0, [0.95, 0.5, 1.0], [1.05, 1.2, 0.8], hists, [0.3, 0.6, 0.9])
+    say(f"[counts16-odd] rows={w.B} V={V}")
+    ref = run_oracle(oracle, w)
+    tok, st, probs = run_gpu(w, cuda)
+    check(w, ref, tok, st, probs)
