@@ -224,6 +224,15 @@ template <typename T> __device__ __forceinline__ T wave_sum(T v)
 }
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) { return wave_max<uint32_t>(v); }
 __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) { return wave_sum<uint32_t>(v); }
+// The sum of v < 2^63 over the wave as three 32-bit sums of 21-bit parts
+// (each part's sum stays below 2^27).
+__device__ __forceinline__ u64 wave_sum_u64(u64 v)
+{
+    const uint32_t a = wave_sum_u32((uint32_t)v & 0x1FFFFFu);
+    const uint32_t b = wave_sum_u32((uint32_t)(v >> 21) & 0x1FFFFFu);
+    const uint32_t c = wave_sum_u32((uint32_t)(v >> 42));
+    return (u64)a + ((u64)b << 21) + ((u64)c << 42);
+}
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v)
 {
     return lane63(wave_prefix_op<uint32_t>(v, 0xFFFFFFFFu, [](uint32_t a, uint32_t b) { return a < b ? a : b; }));

@@ -1550,22 +1550,28 @@ __device__ __forceinline__ bool finish_wide(const Params& p, int r, float T, boo
 //
 // The counts overwrite the history bitmap and list, which are rebuilt when
 // a row falls back to the general path: a rank holding 65536 or more
-// elements, or more than GCAP history ids placed in one chunk.
+// elements, or a draw or cut among more than GCAP history values that lie
+// between the same two ranks.
 //
 // Ranks: R = h ^ KP for an fp16 pattern h >= 0, h ^ KN for h < 0, with
 // (KP, KN) = (0x7FFF, 0) for T > 0 and (0x8000, 0xFFFF) for T < 0.  R < 0x3FF
 // and R > 0xFC00 are NaN patterns, 0x3FF holds the value +inf and 0xFC00 the
 // value -inf; ranks 0x7FFF and 0x8000 both hold 0 and the counts of 0x8000
 // move to 0x7FFF after the pass.
-constexpr int KC_CS = 131072;               // 512 x u64: mass of each chunk of 128 ranks
-constexpr int KC_HS = KC_CS + 4096;         // 512 x u64: penalized history mass placed in each chunk
-constexpr int KC_G = KC_HS + 4096;          // the history ids placed in one chunk
+constexpr int RCH = 256;                    // ranks per chunk: four per lane of a wave
+constexpr int NCH = 65536 / RCH;            // chunks
+constexpr int KC_CS = 131072;               // NCH x u64: mass of each chunk
+constexpr int KC_HS = KC_CS + 8 * NCH;      // NCH x u64: penalized history mass placed in each chunk
+constexpr int KC_G = KC_HS + 8 * NCH;       // history values between two ranks: values, ids, masses
 constexpr int GCAP = 256;
+constexpr int KC_PM = KC_G + 16 * GCAP;     // RCH x u64: history mass placed at each rank of one chunk
+constexpr int KC_PN = KC_PM + 8 * RCH;      // RCH x u32: history values tied with each rank of one chunk
 constexpr int HQ = 4;
 constexpr uint32_t RK_PINF = 0x3FFu, RK_NINF = 0xFC00u, RK_ZERO = 0x7FFFu;
 constexpr int FC_MIN_V = 32768;             // shorter rows take the general path
-static_assert(KC_G + 20 * GCAP <= KF_LDS_BYTES, "chunk history list");
+static_assert(KC_PN + 4 * RCH <= KF_LDS_BYTES, "chunk history arrays");
 static_assert(HCAP <= HQ * NT, "history ids held in registers");
+static_assert(RCH == 256 && NCH <= NT, "chunk layout");
 static_assert(MXS_MAX_VOCAB / 8 <= 32768, "two index bitmaps in the counts' area");
 
 // An element at a mass position of the sorted order.
@@ -1595,8 +1601,9 @@ __device__ __forceinline__ bool finish_counts(const Params& p, int r, RowStream<
                                               uint32_t* hl, uint32_t nh, unsigned char* smem,
                                               int64_t& tok, int32_t& st)
 {
-    __shared__ uint32_t s_csum, s_flag, s_ng, s_own, s_rtop, s_nb;
-    __shared__ u64 s_ownE;
+    __shared__ uint32_t s_csum, s_flag, s_ng, s_own, s_rtop, s_nb, s_bR, s_bflag;
+    __shared__ float s_bl;
+    __shared__ u64 s_ownE, s_btb;
     __shared__ CPick s_pick;
     const int tid = threadIdx.x, lane = lane_id();
     const int V = p.V;
@@ -1604,10 +1611,11 @@ __device__ __forceinline__ bool finish_counts(const Params& p, int r, RowStream<
     uint32_t* cnt = (uint32_t*)smem;
     u64* CS = (u64*)(smem + KC_CS);
     u64* HS = (u64*)(smem + KC_HS);
-    uint32_t* GR = (uint32_t*)(smem + KC_G);
-    float* GL = (float*)(smem + KC_G + 4 * GCAP);
-    uint32_t* GI = (uint32_t*)(smem + KC_G + 8 * GCAP);
-    u64* GW = (u64*)(smem + KC_G + 12 * GCAP);
+    float* GL = (float*)(smem + KC_G);
+    uint32_t* GI = (uint32_t*)(smem + KC_G + 4 * GCAP);
+    u64* GW = (u64*)(smem + KC_G + 8 * GCAP);
+    u64* PM = (u64*)(smem + KC_PM);
+    uint32_t* PN = (uint32_t*)(smem + KC_PN);
     const uint32_t KP = neg ? 0x8000u : 0x7FFFu, KN = neg ? 0xFFFFu : 0u;
     const uint32_t KPAIR = KP * 0x10001u;
     const uint32_t XA = neg ? 0xFFFFu : 0x7FFFu, XB = neg ? 0x8000u : 0u;   // inverse: h = R ^ (R < 0x8000 ? XA : XB)
@@ -1653,7 +1661,7 @@ __device__ __forceinline__ bool finish_counts(const Params& p, int r, RowStream<
         uint4* c4 = (uint4*)smem;
 #pragma unroll
         for (int i = 0; i < KC_CS / 16 / NT; ++i) c4[tid + i * NT] = uint4{0u, 0u, 0u, 0u};
-        HS[tid] = 0;
+        if (tid < NCH) HS[tid] = 0;
         if (tid == 0) { s_csum = 0; s_flag = 0; s_ng = 0; s_own = 0xFFFFFFFFu; }
     }
     __syncthreads();
@@ -1735,18 +1743,24 @@ __device__ __forceinline__ bool finish_counts(const Params& p, int r, RowStream<
     // each history value's place: the last rank whose value is >= it, from
     // the rank of fp16(l * T) (the place itself or a neighbour)
     {
-        float va[HQ], vb[HQ];
+        float va[HQ], vb[HQ], vc[HQ];   // the values of ranks R - 1, R, R + 1
 #pragma unroll
         for (int q = 0; q < HQ; ++q) {
-            hR[q] = rank_of((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(hv[q] * T)));
-            va[q] = val_of(hR[q]);
-            vb[q] = hR[q] < 0xFFFFu ? val_of(hR[q] + 1u) : -INFINITY;
+            uint32_t R = rank_of((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(hv[q] * T)));
+            R = R < 1u ? 1u : (R > 0xFFFEu ? 0xFFFEu : R);
+            hR[q] = R;
+            va[q] = val_of(R - 1u);
+            vb[q] = val_of(R);
+            vc[q] = val_of(R + 1u);
         }
 #pragma unroll
         for (int q = 0; q < HQ; ++q) {
             uint32_t R = hR[q];
             const float l = hv[q];
-            if (hid[q] >= 0 && !(va[q] >= l && !(vb[q] >= l))) {
+            if (vb[q] >= l && !(vc[q] >= l)) {
+            } else if (va[q] >= l && !(vb[q] >= l)) {
+                R -= 1u;
+            } else if (hid[q] >= 0) {
                 while (R > 0u && val_of(R) < l) --R;
                 while (R < 0xFFFFu && val_of(R + 1u) >= l) ++R;
             }
@@ -1754,19 +1768,22 @@ __device__ __forceinline__ bool finish_counts(const Params& p, int r, RowStream<
         }
     }
 
-    // sampling.py:57-58: the masses, per chunk of 128 ranks
+    // sampling.py:57-58: the masses, per chunk of RCH ranks (chunks dealt
+    // round-robin to the waves; a wave skips a chunk with no elements)
     {
         uint32_t csum = 0, nanb = 0;
-        for (int c = wave_id(); c < 512; c += NWAVES) {
-            const uint32_t wd = cnt[64 * c + lane];
+        for (int c = wave_id(); c < NCH; c += NWAVES) {
+            const uint2 wd = *(const uint2*)&cnt[(RCH / 2) * c + 2 * lane];
             u64 acc = 0;
-            if (__ballot(wd != 0u)) {
-                const uint32_t R0 = 128u * (uint32_t)c + 2u * (uint32_t)lane;
-                const uint32_t c0 = wd & 0xFFFFu, c1 = wd >> 16;
-                acc = count_mass(c0, val_fin(R0) - m) + count_mass(c1, val_fin(R0 + 1u) - m);
-                csum += c0 + c1;
-                nanb |= ((R0 > RK_NINF && c0) || (R0 + 1u > RK_NINF && c1)) ? 1u : 0u;
-                acc = wave_sum<u64>(acc);
+            if (__ballot((wd.x | wd.y) != 0u)) {
+                const uint32_t R0 = (uint32_t)(RCH * c) + 4u * (uint32_t)lane;
+                const uint32_t k0 = wd.x & 0xFFFFu, k1 = wd.x >> 16, k2 = wd.y & 0xFFFFu, k3 = wd.y >> 16;
+                acc = count_mass(k0, val_fin(R0) - m) + count_mass(k1, val_fin(R0 + 1u) - m) +
+                      count_mass(k2, val_fin(R0 + 2u) - m) + count_mass(k3, val_fin(R0 + 3u) - m);
+                csum += k0 + k1 + k2 + k3;
+                // (RK_NINF is a multiple of 4: the ranks above it are NaN values)
+                nanb |= R0 > RK_NINF ? (wd.x | wd.y) : (R0 == RK_NINF ? (k1 | wd.y) : 0u);
+                acc = wave_sum_u64(acc);
             }
             if (lane == 0) CS[c] = acc;
         }
@@ -1775,90 +1792,110 @@ __device__ __forceinline__ bool finish_counts(const Params& p, int r, RowStream<
         if (__ballot(nanb != 0u) && lane == 0) atomicOr(&s_flag, NANB);
 #pragma unroll
         for (int q = 0; q < HQ; ++q)
-            if (hid[q] >= 0) atomicAdd(&HS[hR[q] >> 7], mass_of(hv[q] - m));
+            if (hid[q] >= 0) atomicAdd(&HS[hR[q] / RCH], mass_of(hv[q] - m));
     }
     __syncthreads();
     if (s_csum != (uint32_t)V - nhe || (s_flag & OVF)) { restore(); return false; }
     if (s_flag & NANB) { st = MXS_ROW_NONFINITE; tok = -1; return true; }
-    const u64 S = CS[tid] + HS[tid];
+    const u64 S = tid < NCH ? CS[tid] + HS[tid] : 0ull;
     u64 W;
     const u64 E0 = block_incl_scan<u64>(S, &W) - S;
 
-    // The element at mass position t < W.
+    // The element at mass position t < W: the chunk holding t; its ranks'
+    // masses (count x mass, and the penalized history placed there, added
+    // per rank with LDS atomics) in wave 0; if t falls on history values
+    // between two ranks, those values ranked among themselves.
     auto pick = [&](u64 t) -> CPick {
+        if (tid < RCH) { PM[tid] = 0; PN[tid] = 0; }
         if (E0 <= t && t - E0 < S) { s_own = (uint32_t)tid; s_ownE = E0; }
-        if (tid == 0) { s_ng = 0; s_pick.ok = 0; }
+        if (tid == 0) { s_ng = 0; s_pick.ok = 0; s_bflag = 0; }
         __syncthreads();
         const uint32_t c = s_own;
         const u64 Ec = s_ownE;
-        if (c < 512u) {
+#pragma unroll
+        for (int q = 0; q < HQ; ++q)
+            if (hid[q] >= 0 && hR[q] / RCH == c) {
+                const uint32_t o = hR[q] % RCH;
+                atomicAdd(&PM[o], mass_of(hv[q] - m));
+                if (hv[q] == val_of(hR[q])) atomicAdd(&PN[o], 1u);
+            }
+        __syncthreads();
+        if (tid == 0) s_own = 0xFFFFFFFFu;
+        if (c < (uint32_t)NCH && wave_id() == 0) {
+            const u64 tr = t - Ec;
+            const uint32_t R0 = (uint32_t)RCH * c + 4u * (uint32_t)lane;
+            const uint2 wd = *(const uint2*)&cnt[R0 >> 1];
+            const uint32_t kc[4] = {wd.x & 0xFFFFu, wd.x >> 16, wd.y & 0xFFFFu, wd.y >> 16};
+            uint32_t n[4];   // tie groups
+            float lv[4];
+            u64 wv[4], M[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                lv[j] = val_of(R0 + (uint32_t)j);
+                wv[j] = mass_of(lv[j] - m);
+                n[j] = kc[j] + PN[4 * lane + j];
+                M[j] = (u64)kc[j] * wv[j] + PM[4 * lane + j];
+            }
+            const u64 tot = M[0] + M[1] + M[2] + M[3];
+            const u64 incl = wave_prefix_u64(tot);
+            const u64 P = incl - tot;
+            const bool here = P <= tr && tr < incl;
+            if (here) {
+                u64 t2 = tr - P;
+                uint32_t R = R0 + 3u;
+                float lR = lv[3];
+                u64 wR = wv[3];
+                uint32_t nR = n[3];
+                bool found = false;
+#pragma unroll
+                for (int j = 0; j < 3; ++j) {
+                    if (!found && t2 < M[j]) { found = true; R = R0 + (uint32_t)j; lR = lv[j]; wR = wv[j]; nR = n[j]; }
+                    if (!found) t2 -= M[j];
+                }
+                const u64 tie = (u64)nR * wR;
+                if (t2 < tie) {
+                    const u64 i = udiv_est(t2, wR);
+                    s_pick = CPick{t - (t2 - i * wR), wR, i, R, 0xFFFFFFFFu, lR, 1u};
+                } else {   // a penalized history value strictly between ranks R and R + 1
+                    s_bR = R; s_bl = lR; s_btb = t2 - tie; s_bflag = 1u;
+                }
+            }
+        }
+        __syncthreads();
+        if (s_bflag) {
+            // those placed after rank Rs, in order of (value desc, index asc)
+            const uint32_t Rs = s_bR;
+            const float ls = s_bl;
+            const u64 tb = s_btb;
 #pragma unroll
             for (int q = 0; q < HQ; ++q)
-                if (hid[q] >= 0 && (hR[q] >> 7) == c) {
+                if (hid[q] >= 0 && hR[q] == Rs && hv[q] < ls) {
                     const uint32_t g = atomicAdd(&s_ng, 1u);
-                    if (g < (uint32_t)GCAP) {
-                        GR[g] = hR[q]; GL[g] = hv[q]; GI[g] = (uint32_t)hid[q]; GW[g] = mass_of(hv[q] - m);
-                    }
+                    if (g < (uint32_t)GCAP) { GL[g] = hv[q]; GI[g] = (uint32_t)hid[q]; GW[g] = mass_of(hv[q] - m); }
                 }
-        }
-        __syncthreads();
-        const uint32_t ng = s_ng;
-        if (tid == 0) s_own = 0xFFFFFFFFu;
-        if (c < 512u && ng <= (uint32_t)GCAP && wave_id() == 0) {
-            const u64 tr = t - Ec;
-            const uint32_t R0 = 128u * c + 2u * (uint32_t)lane;
-            const uint32_t wd = cnt[R0 >> 1];
-            const float l0 = val_of(R0), l1 = val_of(R0 + 1u);
-            const u64 w0 = mass_of(l0 - m), w1 = mass_of(l1 - m);
-            u64 M0 = (u64)(wd & 0xFFFFu) * w0, M1 = (u64)(wd >> 16) * w1;
-            uint32_t n0 = wd & 0xFFFFu, n1 = wd >> 16;   // tie groups
-            for (uint32_t g = 0; g < ng; ++g) {
-                const uint32_t gr = GR[g];
-                if (gr == R0) { M0 += GW[g]; n0 += GL[g] == l0 ? 1u : 0u; }
-                if (gr == R0 + 1u) { M1 += GW[g]; n1 += GL[g] == l1 ? 1u : 0u; }
-            }
-            const u64 incl = wave_prefix_u64(M0 + M1);
-            const u64 P = incl - (M0 + M1);
-            const bool here = P <= tr && tr < incl;
-            const u64 hm = __ballot(here);
-            if (hm) {
-                const int fl = __builtin_ctzll(hm);
-                u64 t2 = tr - P;
-                const bool second = t2 >= M0;
-                t2 -= second ? M0 : 0ull;
-                const uint32_t R = second ? R0 + 1u : R0;
-                const float lR = second ? l1 : l0;
-                const u64 wR = second ? w1 : w0;
-                const u64 tie = (u64)(second ? n1 : n0) * wR;
-                const uint32_t Rs = (uint32_t)__builtin_amdgcn_readlane((int)R, fl);
-                const float ls = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lR), fl));
-                const bool in_tie = __builtin_amdgcn_readlane(t2 < tie ? 1 : 0, fl) != 0;
-                if (in_tie) {
-                    if (here) {
-                        const u64 i = udiv_est(t2, wR);
-                        s_pick = CPick{t - (t2 - i * wR), wR, i, R, 0xFFFFFFFFu, lR, 1u};
-                    }
-                } else {
-                    // a penalized history value strictly between ranks Rs and Rs + 1:
-                    // those there in order of (value desc, index asc)
-                    const u64 tb = readlane64(t2 - tie, fl);
-                    for (uint32_t g0 = 0; g0 < ng; g0 += 64u) {
-                        const uint32_t g = g0 + (uint32_t)lane;
-                        if (g < ng && GR[g] == Rs && GL[g] < ls) {
-                            const u64 key = ((u64)vkey(GL[g]) << 32) | (u64)(0xFFFFFFFFu - GI[g]);
-                            u64 Eh = 0;
-                            for (uint32_t g2 = 0; g2 < ng; ++g2) {
-                                const u64 k2 = ((u64)vkey(GL[g2]) << 32) | (u64)(0xFFFFFFFFu - GI[g2]);
-                                if (GR[g2] == Rs && GL[g2] < ls && k2 > key) Eh += GW[g2];
-                            }
-                            if (Eh <= tb && tb - Eh < GW[g])
-                                s_pick = CPick{t - (tb - Eh), GW[g], 0ull, Rs, GI[g], GL[g], 1u};
+            __syncthreads();
+            const uint32_t ng = s_ng;
+            if (ng <= (uint32_t)GCAP && wave_id() == 0) {
+                auto key_at = [&](uint32_t g) { return ((u64)vkey(GL[g]) << 32) | (u64)(0xFFFFFFFFu - GI[g]); };
+                for (uint32_t g0 = 0; g0 < ng; g0 += 64u) {
+                    const uint32_t g = g0 + (uint32_t)lane;
+                    const bool cand = g < ng;
+                    const u64 key = cand ? key_at(g) : 0ull, wg = cand ? GW[g] : 0ull;
+                    u64 Eh = 0;   // the mass of those ranked before it
+                    for (uint32_t g1 = 0; g1 < ng; g1 += 64u) {
+                        const uint32_t g2 = g1 + (uint32_t)lane;
+                        const bool in2 = g2 < ng;
+                        const u64 k2 = in2 ? key_at(g2) : 0ull, w2 = in2 ? GW[g2] : 0ull;
+                        for (u64 msk = __ballot(in2); msk; msk &= msk - 1ull) {
+                            const int b = __builtin_ctzll(msk);
+                            Eh += readlane64(k2, b) > key ? readlane64(w2, b) : 0ull;
                         }
                     }
+                    if (cand && Eh <= tb && tb - Eh < wg) s_pick = CPick{t - tb + Eh, wg, 0ull, Rs, GI[g], GL[g], 1u};
                 }
             }
+            __syncthreads();
         }
-        __syncthreads();
         const CPick res = s_pick;
         __syncthreads();
         return res;
