@@ -101,6 +101,26 @@ int mxs_sample(const void* logits, int dtype, int B, int V, int64_t ld,
                int64_t* out_tokens, int32_t* out_status, float* out_probs,
                void* workspace, size_t workspace_bytes, mxs_stream_t stream);
 
+/*
+ * mxs_sample with each row's history given as a range of a caller-owned id
+ * buffer: row r's generated ids are hist_ids[hist_begin[r], hist_end[r])
+ * (an empty range when hist_end[r] <= hist_begin[r]).  Ranges may overlap
+ * and need not be in row order, so a buffer that holds every request's
+ * generated ids at fixed places on the device serves any subset of the
+ * requests without repacking.  It replaces the per-step rebuild of each
+ * request's history from req.output_ids (mini_engine/scheduler.py:43, 275-276,
+ * consumed at mini_engine/sampling.py:38-45).  hist_begin and hist_end are
+ * both i32[B] device arrays, or both NULL for no history; everything else is
+ * as for mxs_sample.
+ */
+int mxs_sample_ranges(const void* logits, int dtype, int B, int V, int64_t ld,
+                      const float* temperature, const int32_t* top_k,
+                      const float* top_p, const float* penalty,
+                      const int32_t* hist_begin, const int32_t* hist_end, const int32_t* hist_ids,
+                      const float* uniforms,
+                      int64_t* out_tokens, int32_t* out_status, float* out_probs,
+                      void* workspace, size_t workspace_bytes, mxs_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

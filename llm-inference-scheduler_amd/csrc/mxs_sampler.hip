@@ -36,8 +36,9 @@ struct Params {
     const int32_t* K;
     const float* P;
     const float* PEN;
-    const int32_t* hoff;
+    const int32_t* hoff;   // row r's history: hids[hoff[r], hend ? hend[r] : hoff[r + 1])
     const int32_t* hids;
+    const int32_t* hend;
     const float* U;
     int64_t* out_tok;
     int32_t* out_status;
@@ -2091,7 +2092,7 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
     pa = lane == 2 ? (const uint32_t*)(p.PEN + r) : pa;
     pa = lane == 3 ? (const uint32_t*)(p.P + r) : pa;
     pa = (lane == 4 && p.hoff) ? (const uint32_t*)(p.hoff + r) : pa;
-    pa = (lane == 5 && p.hoff) ? (const uint32_t*)(p.hoff + r + 1) : pa;
+    pa = (lane == 5 && p.hoff) ? (const uint32_t*)(p.hend ? p.hend + r : p.hoff + r + 1) : pa;
     pa = (lane == 6 && p.U) ? (const uint32_t*)(p.U + r) : pa;
     const uint32_t pv = *pa;
     // The sample: NSAMP logits in 64 groups of 32 consecutive ones spread
@@ -2766,13 +2767,19 @@ size_t mxs_workspace_bytes(int B, int V)
     return WORKSPACE_BYTES;
 }
 
-int mxs_sample(const void* logits, int dtype, int B, int V, int64_t ld,
-               const float* temperature, const int32_t* top_k,
-               const float* top_p, const float* penalty,
-               const int32_t* hist_offsets, const int32_t* hist_ids,
-               const float* uniforms,
-               int64_t* out_tokens, int32_t* out_status, float* out_probs,
-               void* workspace, size_t workspace_bytes, mxs_stream_t stream)
+}  // extern "C"
+
+namespace {
+
+// Both entry points: the history of row r is hist_ids[hbegin[r], hend[r]),
+// with hend == NULL meaning CSR (hend[r] = hbegin[r + 1]).
+int sample_impl(const void* logits, int dtype, int B, int V, int64_t ld,
+                const float* temperature, const int32_t* top_k,
+                const float* top_p, const float* penalty,
+                const int32_t* hbegin, const int32_t* hend, const int32_t* hist_ids,
+                const float* uniforms,
+                int64_t* out_tokens, int32_t* out_status, float* out_probs,
+                void* workspace, size_t workspace_bytes, mxs_stream_t stream)
 {
     if (B < 0 || V <= 0) return MXS_ERR_INVALID_ARGUMENT;
     if (V > MXS_MAX_VOCAB) return MXS_ERR_VOCAB_TOO_LARGE;
@@ -2780,7 +2787,7 @@ int mxs_sample(const void* logits, int dtype, int B, int V, int64_t ld,
     if (B == 0) return MXS_OK;
     if (!logits || !temperature || !top_k || !top_p || !penalty || !out_tokens || !workspace)
         return MXS_ERR_INVALID_ARGUMENT;
-    if (hist_offsets && !hist_ids) return MXS_ERR_INVALID_ARGUMENT;
+    if (hbegin && !hist_ids) return MXS_ERR_INVALID_ARGUMENT;
     if (ld < V) return MXS_ERR_INVALID_ARGUMENT;
     const uintptr_t esize = dtype == MXS_DTYPE_F32 ? 4u : 2u;
     if (((uintptr_t)logits & (esize - 1u)) || ((uintptr_t)workspace & 255u)) return MXS_ERR_ALIGNMENT;
@@ -2795,8 +2802,9 @@ int mxs_sample(const void* logits, int dtype, int B, int V, int64_t ld,
     p.K = top_k;
     p.P = top_p;
     p.PEN = penalty;
-    p.hoff = hist_offsets;
+    p.hoff = hbegin;
     p.hids = hist_ids;
+    p.hend = hbegin ? hend : nullptr;
     p.U = uniforms;
     p.out_tok = out_tokens;
     p.out_status = out_status;
@@ -2805,6 +2813,35 @@ int mxs_sample(const void* logits, int dtype, int B, int V, int64_t ld,
     hipStream_t s = (hipStream_t)stream;
     hipError_t e = dtype == MXS_DTYPE_F32 ? launch<float>(p, s) : launch<__half>(p, s);
     return e == hipSuccess ? MXS_OK : MXS_ERR_HIP;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mxs_sample(const void* logits, int dtype, int B, int V, int64_t ld,
+               const float* temperature, const int32_t* top_k,
+               const float* top_p, const float* penalty,
+               const int32_t* hist_offsets, const int32_t* hist_ids,
+               const float* uniforms,
+               int64_t* out_tokens, int32_t* out_status, float* out_probs,
+               void* workspace, size_t workspace_bytes, mxs_stream_t stream)
+{
+    return sample_impl(logits, dtype, B, V, ld, temperature, top_k, top_p, penalty, hist_offsets, nullptr,
+                       hist_ids, uniforms, out_tokens, out_status, out_probs, workspace, workspace_bytes, stream);
+}
+
+int mxs_sample_ranges(const void* logits, int dtype, int B, int V, int64_t ld,
+                      const float* temperature, const int32_t* top_k,
+                      const float* top_p, const float* penalty,
+                      const int32_t* hist_begin, const int32_t* hist_end, const int32_t* hist_ids,
+                      const float* uniforms,
+                      int64_t* out_tokens, int32_t* out_status, float* out_probs,
+                      void* workspace, size_t workspace_bytes, mxs_stream_t stream)
+{
+    if ((hist_begin != nullptr) != (hist_end != nullptr)) return MXS_ERR_INVALID_ARGUMENT;
+    return sample_impl(logits, dtype, B, V, ld, temperature, top_k, top_p, penalty, hist_begin, hist_end,
+                       hist_ids, uniforms, out_tokens, out_status, out_probs, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

@@ -95,6 +95,54 @@ void sample(torch::Tensor logits, torch::Tensor temperature, torch::Tensor top_k
     raise_status(st, "mxs_sample");
 }
 
+// The same launch with row r's history at hist_ids[hist_begin[r], hist_end[r])
+// (mxs_sample_ranges): hist_ids may be a buffer that stays on the device.
+void sample_ranges(torch::Tensor logits, torch::Tensor temperature, torch::Tensor top_k,
+                   torch::Tensor top_p, torch::Tensor penalty,
+                   torch::Tensor hist_begin, torch::Tensor hist_end, torch::Tensor hist_ids,
+                   std::optional<torch::Tensor> uniforms, torch::Tensor out_tokens,
+                   std::optional<torch::Tensor> out_status, std::optional<torch::Tensor> out_probs,
+                   torch::Tensor workspace)
+{
+    TORCH_CHECK(logits.is_cuda(), "logits must be on a GPU device");
+    TORCH_CHECK(logits.dim() == 2, "logits must be [B, V]");
+    TORCH_CHECK(logits.stride(1) == 1, "logits rows must be contiguous");
+    const int64_t B = logits.size(0), V = logits.size(1);
+    int dtype;
+    if (logits.scalar_type() == torch::kFloat32) dtype = MXS_DTYPE_F32;
+    else if (logits.scalar_type() == torch::kFloat16) dtype = MXS_DTYPE_F16;
+    else TORCH_CHECK(false, "logits must be float32 or float16, got ", logits.scalar_type());
+
+    check_dev(temperature, logits, "temperature", torch::kFloat32, B);
+    check_dev(top_k, logits, "top_k", torch::kInt32, B);
+    check_dev(top_p, logits, "top_p", torch::kFloat32, B);
+    check_dev(penalty, logits, "penalty", torch::kFloat32, B);
+    check_dev(hist_begin, logits, "hist_begin", torch::kInt32, B);
+    check_dev(hist_end, logits, "hist_end", torch::kInt32, B);
+    check_dev(hist_ids, logits, "hist_ids", torch::kInt32, -1);
+    TORCH_CHECK(hist_ids.numel() > 0, "hist_ids must not be empty");
+    if (uniforms) check_dev(*uniforms, logits, "uniforms", torch::kFloat32, B);
+    check_dev(out_tokens, logits, "out_tokens", torch::kInt64, B);
+    if (out_status) check_dev(*out_status, logits, "out_status", torch::kInt32, B);
+    if (out_probs) check_dev(*out_probs, logits, "out_probs", torch::kFloat32, B * V);
+    TORCH_CHECK(workspace.device() == logits.device() && workspace.is_contiguous() &&
+                workspace.scalar_type() == torch::kUInt8, "workspace must be a uint8 tensor on the logits device");
+
+    const c10::DeviceGuard guard(logits.device());
+    auto stream = c10::hip::getCurrentHIPStream();
+    int st = mxs_sample_ranges(logits.data_ptr(), dtype, (int)B, (int)V, logits.stride(0),
+                               temperature.data_ptr<float>(), top_k.data_ptr<int32_t>(),
+                               top_p.data_ptr<float>(), penalty.data_ptr<float>(),
+                               hist_begin.data_ptr<int32_t>(), hist_end.data_ptr<int32_t>(),
+                               hist_ids.data_ptr<int32_t>(),
+                               (const float*)opt_ptr(uniforms), out_tokens.data_ptr<int64_t>(),
+                               out_status ? out_status->data_ptr<int32_t>() : nullptr,
+                               out_probs ? out_probs->data_ptr<float>() : nullptr,
+                               workspace.data_ptr(), (size_t)workspace.numel(),
+                               (mxs_stream_t)stream.stream());
+    raise_status(st, "mxs_sample_ranges");
+}
+
 std::string version() { return mxs_version(); }
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m)
@@ -106,4 +154,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m)
           py::arg("logits"), py::arg("temperature"), py::arg("top_k"), py::arg("top_p"),
           py::arg("penalty"), py::arg("hist_offsets"), py::arg("hist_ids"), py::arg("uniforms"),
           py::arg("out_tokens"), py::arg("out_status"), py::arg("out_probs"), py::arg("workspace"));
+    m.def("sample_ranges", &sample_ranges,
+          "sample one token per row, histories as [begin, end) ranges of a device id buffer",
+          py::arg("logits"), py::arg("temperature"), py::arg("top_k"), py::arg("top_p"),
+          py::arg("penalty"), py::arg("hist_begin"), py::arg("hist_end"), py::arg("hist_ids"),
+          py::arg("uniforms"), py::arg("out_tokens"), py::arg("out_status"), py::arg("out_probs"),
+          py::arg("workspace"));
 }

@@ -2,18 +2,21 @@
 top-k, top-p, softmax, draw) for the reference engine's
 mini_engine/sampling.py, on hand-written gfx950 HIP kernels.
 
-  SamplingParams, sample   drop-in for mini_engine/sampling.py:15-69
-  sample_batch             one launch for a [B, V] batch, per-row device params
-  sample_requests          batch from per-request SamplingParams / histories
+  SamplingParams, sample     drop-in for mini_engine/sampling.py:15-69
+  sample_batch               one launch for a [B, V] batch, per-row device params
+  sample_requests            batch from per-request SamplingParams / histories
+  HistoryStore               requests' generated ids kept on the device across steps
+  sample_requests_resident   sample_requests reading the histories from a HistoryStore
 """
 
 from .batch import (MAX_VOCAB, ROW_BAD_HISTORY, ROW_BAD_PARAM, ROW_EMPTY_NUCLEUS,
-                    ROW_NONFINITE, ROW_OK, Sampler, pack_requests, sample_batch,
-                    sample_requests)
+                    ROW_NONFINITE, ROW_OK, HistoryStore, Sampler, pack_requests, pack_resident,
+                    sample_batch, sample_batch_ranges, sample_requests, sample_requests_resident)
 from .sampling import SamplingParams, sample
 
 __all__ = [
     "SamplingParams", "sample", "sample_batch", "Sampler", "sample_requests", "pack_requests",
+    "HistoryStore", "sample_batch_ranges", "sample_requests_resident", "pack_resident",
     "MAX_VOCAB", "ROW_OK", "ROW_BAD_HISTORY", "ROW_BAD_PARAM", "ROW_NONFINITE",
     "ROW_EMPTY_NUCLEUS",
 ]

@@ -4,6 +4,8 @@
 history as CSR); `sample_requests` packs a scheduler's per-request
 SamplingParams, output ids and generators into that form (the batched
 counterpart of the per-row loop at mini_engine/scheduler.py:268-275).
+`HistoryStore` keeps the requests' generated ids on the device across steps,
+and `sample_requests_resident` / `sample_batch_ranges` read them there.
 """
 
 from __future__ import annotations
@@ -139,6 +141,148 @@ def sample_requests(logits: torch.Tensor, params_list, histories, generators=Non
     for r, s in enumerate(st):
         if s != ROW_OK:
             raise_row_status(s, r)
+    return tokens.cpu().tolist()
+
+
+def sample_batch_ranges(logits: torch.Tensor, temperature: torch.Tensor, top_k: torch.Tensor,
+                        top_p: torch.Tensor, penalty: torch.Tensor, hist_begin: torch.Tensor,
+                        hist_end: torch.Tensor, hist_ids: torch.Tensor,
+                        uniforms: Optional[torch.Tensor] = None,
+                        out_probs: Optional[torch.Tensor] = None,
+                        return_status: bool = False):
+    """sample_batch with row r's history at hist_ids[hist_begin[r], hist_end[r])
+    (i32[B] each, on the device): hist_ids can stay on the device across
+    steps (HistoryStore).  The launch is asynchronous on the current stream."""
+    _native.require_gpu(logits.device)
+    ext = _native.extension()
+    B, V = logits.shape
+    dev = logits.device
+    tokens = torch.empty(B, dtype=torch.int64, device=dev)
+    status = torch.empty(B, dtype=torch.int32, device=dev)
+    ws = _native.workspace(dev, B, V)
+    ext.sample_ranges(logits, temperature, top_k, top_p, penalty, hist_begin, hist_end, hist_ids,
+                      uniforms, tokens, status, out_probs, ws)
+    return (tokens, status) if return_status else tokens
+
+
+class HistoryStore:
+    """Generated token ids of up to `slots` requests, resident on the device
+    across decode steps; their lengths are mirrored on the host.
+
+    The reference rebuilds each request's history from its Python list at
+    every step (req.output_ids, mini_engine/scheduler.py:43, appended at :276
+    and read by sampling.py:38-45).  Here request slot s owns
+    ids[s * max_len, (s + 1) * max_len); `append` writes a step's sampled
+    tokens there on the device, so a step sends only each row's range.
+    """
+
+    def __init__(self, slots: int, max_len: int, device):
+        if slots <= 0 or max_len <= 0:
+            raise ValueError("slots and max_len must be positive")
+        if slots * max_len >= 2**31:
+            raise ValueError("slots * max_len must stay below 2^31 (int32 ranges)")
+        self.slots, self.max_len = int(slots), int(max_len)
+        self.device = torch.device(device)
+        self.ids = torch.zeros(self.slots * self.max_len, dtype=torch.int32, device=self.device)
+        self.lens = [0] * self.slots
+
+    def _check_slot(self, slot: int) -> int:
+        slot = int(slot)
+        if not 0 <= slot < self.slots:
+            raise IndexError(f"slot {slot} outside [0, {self.slots})")
+        return slot
+
+    def reset(self, slot: int, ids: Sequence[int] = (), V: Optional[int] = None) -> None:
+        """Start slot `slot` with `ids` (ids it generated before; normalized
+        like sampling.py:39-40 when V is given)."""
+        slot = self._check_slot(slot)
+        ids = _normalize_history(ids, V) if V is not None else [int(i) for i in ids]
+        if len(ids) > self.max_len:
+            raise ValueError(f"{len(ids)} ids exceed max_len {self.max_len}")
+        if ids:
+            b = slot * self.max_len
+            self.ids[b:b + len(ids)] = torch.tensor(ids, dtype=torch.int32).to(self.device)
+        self.lens[slot] = len(ids)
+
+    def append(self, slots: Sequence[int], tokens) -> None:
+        """Append tokens[i] to slot slots[i] (tokens: a device tensor, as
+        returned by the sampler, or a sequence of ints).  Device-side copy;
+        no synchronization."""
+        slots = [self._check_slot(s) for s in slots]
+        if len(set(slots)) != len(slots):
+            raise ValueError("a slot appears twice in one append")
+        pos = []
+        for s in slots:
+            if self.lens[s] >= self.max_len:
+                raise ValueError(f"slot {s} is full ({self.max_len} ids)")
+            pos.append(s * self.max_len + self.lens[s])
+        if not pos:
+            return
+        idx = torch.tensor(pos, dtype=torch.int64).to(self.device)
+        tok = torch.as_tensor(tokens).to(device=self.device, dtype=torch.int32).reshape(-1)
+        if tok.numel() != len(pos):
+            raise ValueError(f"{tok.numel()} tokens for {len(pos)} slots")
+        self.ids.index_copy_(0, idx, tok)
+        for s in slots:
+            self.lens[s] += 1
+
+    def ranges(self, slots: Sequence[int]):
+        """Host lists (begin, end) of the given slots' histories in `ids`."""
+        slots = [self._check_slot(s) for s in slots]
+        return ([s * self.max_len for s in slots],
+                [s * self.max_len + self.lens[s] for s in slots])
+
+    def history(self, slot: int) -> list:
+        """Slot `slot`'s ids, read back (for checks; synchronizes)."""
+        slot = self._check_slot(slot)
+        b = slot * self.max_len
+        return self.ids[b:b + self.lens[slot]].cpu().tolist()
+
+
+def pack_resident(params_list, store: HistoryStore, slots: Sequence[int], device, generators=None):
+    """Device tensors for sample_batch_ranges: the per-row parameters, one
+    uniform per stochastic row (as pack_requests draws them) and each row's
+    history range in store.ids, in one host buffer and one transfer."""
+    B = len(params_list)
+    if len(slots) != B:
+        raise ValueError(f"{len(slots)} slots for {B} rows")
+    gens = generators if generators is not None else [None] * B
+    begin, end = store.ranges(slots)
+    # layout (int32 words): T[B] K[B] P[B] PEN[B] U[B] BEGIN[B] END[B]
+    buf = torch.empty(7 * B, dtype=torch.int32)
+    f = buf.view(torch.float32)
+    for r, (p, g) in enumerate(zip(params_list, gens)):
+        f[r] = float(p.temperature)
+        buf[B + r] = int(p.top_k) if -2**31 <= int(p.top_k) < 2**31 else (2**31 - 1)
+        f[2 * B + r] = float(p.top_p)
+        f[3 * B + r] = float(p.repetition_penalty)
+        f[4 * B + r] = 0.0 if p.temperature == 0.0 else float(torch.rand((), generator=g))
+        buf[5 * B + r] = begin[r]
+        buf[6 * B + r] = end[r]
+    d = buf.to(device, non_blocking=False)
+    df = d.view(torch.float32)
+    return dict(temperature=df[0:B], top_k=d[B:2 * B], top_p=df[2 * B:3 * B],
+                penalty=df[3 * B:4 * B], uniforms=df[4 * B:5 * B],
+                hist_begin=d[5 * B:6 * B], hist_end=d[6 * B:7 * B])
+
+
+def sample_requests_resident(logits: torch.Tensor, params_list, store: HistoryStore,
+                             slots: Sequence[int], generators=None,
+                             out_probs: Optional[torch.Tensor] = None, append: bool = True) -> list:
+    """sample_requests with the histories resident in `store`: row r is the
+    request in slot slots[r].  The sampled tokens are appended to their slots
+    on the device (mini_engine/scheduler.py:276) unless append is False;
+    raises like the reference would for the first failing row, before
+    appending anything."""
+    packed = pack_resident(params_list, store, slots, logits.device, generators)
+    tokens, status = sample_batch_ranges(logits, hist_ids=store.ids, out_probs=out_probs,
+                                         return_status=True, **packed)
+    st = status.cpu().tolist()
+    for r, s in enumerate(st):
+        if s != ROW_OK:
+            raise_row_status(s, r)
+    if append:
+        store.append(slots, tokens)
     return tokens.cpu().tolist()
 
 

@@ -46,12 +46,15 @@ def lib():
     L.mxs_sample.restype = ctypes.c_int
     L.mxs_sample.argtypes = [p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int64,
                              p, p, p, p, p, p, p, p, p, p, p, ctypes.c_size_t, p]
+    L.mxs_sample_ranges.restype = ctypes.c_int
+    L.mxs_sample_ranges.argtypes = [p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int64,
+                                    p, p, p, p, p, p, p, p, p, p, p, p, ctypes.c_size_t, p]
     return L
 
 
 def test_header_declares_the_expected_entry_points():
-    assert declared_functions() == ["mxs_sample", "mxs_status_string", "mxs_version",
-                                    "mxs_workspace_bytes"]
+    assert declared_functions() == ["mxs_sample", "mxs_sample_ranges", "mxs_status_string",
+                                    "mxs_version", "mxs_workspace_bytes"]
 
 
 def test_every_declared_symbol_is_exported(lib):
@@ -124,6 +127,25 @@ def test_sample_rejects_bad_arguments_before_launching(lib):
     assert call(lib, logits=A + 2) == ALIGN                  # f32 rows need 4-byte alignment
     assert call(lib, workspace=A + 64) == ALIGN
     assert call(lib, workspace_bytes=lib.mxs_workspace_bytes(4, 1000) - 1) == SMALL_WS
+
+
+def call_ranges(lib, logits=A, dtype=0, B=4, V=1000, ld=1000, hist_begin=A, hist_end=A,
+                hist_ids=A, out_tokens=A, workspace=A):
+    ws = 0 if B <= 0 or V <= 0 or V > MAX_VOCAB else lib.mxs_workspace_bytes(B, V)
+    return lib.mxs_sample_ranges(P(logits), dtype, B, V, ld, P(A), P(A), P(A), P(A),
+                                 P(hist_begin), P(hist_end), P(hist_ids), P(A), P(out_tokens),
+                                 P(A), P(None), P(workspace), ws, None)
+
+
+def test_sample_ranges_rejects_bad_arguments_before_launching(lib):
+    assert call_ranges(lib, hist_begin=A, hist_end=None) == INVALID   # begin and end go together
+    assert call_ranges(lib, hist_begin=None, hist_end=A) == INVALID
+    assert call_ranges(lib, hist_ids=None) == INVALID                 # ranges need an id buffer
+    assert call_ranges(lib, B=-1) == INVALID
+    assert call_ranges(lib, V=MAX_VOCAB + 1, ld=MAX_VOCAB + 1) == VOCAB
+    assert call_ranges(lib, logits=A + 2) == ALIGN
+    assert call_ranges(lib, out_tokens=None) == INVALID
+    assert call_ranges(lib, B=0, logits=None, out_tokens=None, workspace=None) == OK
 
 
 def test_empty_batch_is_a_no_op(lib):
