@@ -133,7 +133,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
-    ap.add_argument("--cold", action="store_true", help="also time with the MALL flushed")
+    ap.add_argument("--no-cold", action="store_true",
+                    help="skip the timing with the MALL flushed before each call")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="instead of the sampler, time a plain device copy of this many bytes "
                          "(the reference point for HBM byte counters)")
@@ -188,11 +189,13 @@ def main():
     dur_us = np.array([a.elapsed_time(b) * 1e3 for a, b in evs])
 
     cold = None
-    if args.cold:
-        flush = torch.empty(1 << 29, dtype=torch.uint8, device=dev)   # 512 MiB > 256 MiB MALL
+    if not args.no_cold:
+        # 512 MiB > the 256 MiB MALL, read (not written) before each call, so
+        # that the call finds the cache full of clean lines that are not its own
+        flush = torch.ones(1 << 27, dtype=torch.float32, device=dev)
         cd = []
         for _ in range(min(args.steps, 50)):
-            flush.add_(1)
+            flush.sum()
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record(stream)
             run()
