@@ -6,9 +6,9 @@
  *   -> softmax -> draw,
  * the chain of mini_engine/sampling.py:30-69, with per-row parameters passed
  * as device arrays.  Plain pointers and sizes only; every buffer belongs to
- * the caller and the library allocates nothing.  A call enqueues one kernel
- * on `stream` and returns; two calls may run concurrently only with distinct
- * workspaces.
+ * the caller and the library allocates nothing.  A call enqueues its kernels
+ * (one; two for batches of up to 64 rows) on `stream` and returns; two calls
+ * may run concurrently only with distinct workspaces.
  *
  * Results per row (token ids, post-filter probabilities) are defined by the
  * exact arithmetic described in the oracle that the tests check against:
@@ -64,11 +64,12 @@ const char* mxs_version(void);
 const char* mxs_status_string(int status);
 
 /*
- * Workspace size in bytes for a batch of B rows of V logits.  The current
- * kernel keeps every row's state on chip and needs only a token 256 bytes;
- * callers size the buffer with this function so that a later version may use
- * more.  It must be 256-byte aligned; it needs no initialization and its
- * contents need not survive between calls.  Returns 0 for an invalid shape.
+ * Workspace size in bytes for a batch of B rows of V logits (the same for
+ * every valid shape, about 3 MB): batches of up to 64 rows first split each
+ * row across several workgroups, which hand their candidates over in the
+ * workspace; larger batches keep every row's state on chip.  It must be
+ * 256-byte aligned; it needs no initialization and its contents need not
+ * survive between calls.  Returns 0 for an invalid shape.
  */
 size_t mxs_workspace_bytes(int B, int V);
 

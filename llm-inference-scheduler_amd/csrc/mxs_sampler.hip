@@ -43,6 +43,10 @@ struct Params {
     int64_t* out_tok;
     int32_t* out_status;
     float* out_probs;
+    // candidates handed over by k_slices (NULL: none): G slices per row
+    const uint32_t* sl_hdr;
+    const uint32_t* sl_ent;
+    int G;
 };
 
 __device__ __forceinline__ RowMode classify(float T, int k, int V)
@@ -1018,28 +1022,31 @@ struct RowStream {
     int V, nvec, ntile;
     vec_t A[FU], Bf[FU];
 
-    __device__ __forceinline__ RowStream(const TIn* rp, int v) : rowp(rp), V(v)
+    // (issue = false: the first tiles are left for restart(); the loads are
+    // issued all the same, of a dummy vector, since a branch around them
+    // would make the compiler wait for every load in flight)
+    __device__ __forceinline__ RowStream(const TIn* rp, int v, bool issue = true) : rowp(rp), V(v)
     {
         nvec = ((((uintptr_t)rp) & 15u) == 0) ? v / VW : 0;
         ntile = (nvec + TV - 1) / TV;
-        restart();
+        restart(issue);
     }
     // The first two tiles.  The tile numbers pass through an empty asm
     // statement, so that the compiler computes these addresses at each use
     // instead of keeping one set alive (in scratch) for all the passes.
-    __device__ __forceinline__ void restart()
+    __device__ __forceinline__ void restart(bool live = true)
     {
         int t0 = 0;
         asm volatile("" : "+s"(t0));
-        load(A, t0);
-        load(Bf, t0 + 1);
+        load(A, t0, live);
+        load(Bf, t0 + 1, live);
     }
     // (no branch: a row with no whole vector reads a dummy vector instead)
-    __device__ __forceinline__ void load(vec_t (&b)[FU], int t)
+    __device__ __forceinline__ void load(vec_t (&b)[FU], int t, bool live = true)
     {
         typedef const __attribute__((address_space(1))) vec_t* gptr;   // global memory: plain vector loads
-        const gptr src = nvec > 0 ? (gptr)rowp : (gptr)&g_zero_vec;
-        const int lastv = nvec > 0 ? nvec - 1 : 0;
+        const gptr src = (nvec > 0 && live) ? (gptr)rowp : (gptr)&g_zero_vec;
+        const int lastv = (nvec > 0 && live) ? nvec - 1 : 0;
         t = t < ntile ? t : ntile - 1;
         t = t > 0 ? t : 0;
 #pragma unroll
@@ -2030,6 +2037,174 @@ __device__ __forceinline__ bool finish_counts(const Params& p, int r, RowStream<
     return true;
 }
 
+// sampling.py:52-54, step 1 of the top-k path: a conservative estimate est of
+// the row's k-th largest selection key from its NSAMP-logit sample (this
+// thread's NS logits sx, the first at index se0): the lower edge of the
+// histogram bin holding the sample's j-th largest, j well above the expected
+// k * NSAMP / V; and theta = widen(est).  It only steers the stream; the
+// count pass checks it.  hist (2048) and s_cs (64) must be zero; called by
+// the whole workgroup.
+__device__ __forceinline__ void sample_bound(const float (&sx)[NSAMP / NT], int se0, uint32_t kk, int V, float T,
+                                             bool neg, bool pen_inline, float pen, const uint32_t* bm,
+                                             uint32_t* hist, uint32_t* s_cs, uint32_t& est, uint32_t& theta)
+{
+    constexpr int NS = NSAMP / NT;
+    uint32_t sk4[NS], smax = 0, smin = 0xFFFFFFFFu;
+#pragma unroll
+    for (int q = 0; q < NS; ++q) {
+        const int e = se0 + q;   // (< V: rows that sample are long)
+        float x = sx[q];
+        if (pen_inline && ((bm[e >> 5] >> (e & 31)) & 1u)) x = penalize(x, pen);
+        sk4[q] = selkey(x, neg);
+        smax = sk4[q] > smax ? sk4[q] : smax;
+        smin = sk4[q] < smin ? sk4[q] : smin;
+    }
+    const float ks = (float)kk * (float)NSAMP / (float)V;
+    uint32_t js = (uint32_t)ceilf(ks + 6.0f * sqrtf(ks) + 3.0f);
+    js = js < (uint32_t)NSAMP ? js : (uint32_t)NSAMP;
+    const Reduced sr = block_reduce(smax, smin, 0u);   // (its barriers also order the zeroed hist)
+    const uint32_t span = sr.max - sr.min;
+    const int sh = span >= 2048u ? (32 - __builtin_clz(span)) - 11 : 0;
+#pragma unroll
+    for (int q = 0; q < NS; ++q) {
+        const uint32_t b = (sk4[q] - sr.min) >> sh;
+        atomicAdd(&hist[b], 1u);
+        atomicAdd(&s_cs[b >> 5], 1u);
+    }
+    __syncthreads();
+    // (every wave finds the bin by itself)
+    const WHit hb = wave_find_desc<uint32_t>(hist, (u64)s_cs[lane_id()], (u64)(js - 1u));
+    est = sr.min + ((uint32_t)hb.bin << sh);
+    if (est < SK_MIN) est = SK_MIN;
+    theta = widen_threshold(est, T, neg);
+}
+
+// ---------------------------------------------------------------- small batches
+//
+// With few rows, one workgroup per row leaves most CUs idle and each row's
+// stream runs at one CU's share of bandwidth.  For B <= SPLIT_MAX_B a first
+// kernel, k_slices, cuts every top-k row that can defer its penalty (and
+// every greedy row without one) into G slices of consecutive logits, one
+// workgroup per slice.  Every slice computes the row's sampled bound from
+// the same sample with the same code, so all slices agree on it; a slice
+// streams its logits and writes the keys that reach the bound with their
+// ids, its key extremes and the bound (a greedy slice: its packed maximum)
+// to a header and a candidate list in the workspace.  k_fused then loads a
+// row's candidates into its wave segments in place of its own stream and
+// goes on from the count pass; a row with a full slice, or one k_slices did
+// not take, streams in k_fused as usual.
+constexpr int SPLIT_MAX_B = 64;
+constexpr int SPLIT_SLICES = 256;              // B * G at most
+constexpr int SLICE_CAP = FSEG - 64;           // candidates of one slice (a wave segment's room)
+constexpr int SL_HDR = 8;                      // header words: n, key max, key min, est, theta, best lo, best hi
+constexpr uint32_t SL_NONE = 0xFFFFFFFFu;      // n of a slice that hands over nothing
+constexpr size_t SL_HDR_BYTES = (size_t)SPLIT_SLICES * SL_HDR * 4;
+constexpr size_t SL_WS_BYTES = SL_HDR_BYTES + (size_t)SPLIT_SLICES * SLICE_CAP * 8;
+
+__host__ __device__ __forceinline__ int split_slices(int B) { return B <= 4 ? 64 : SPLIT_SLICES / B; }
+static_assert(SPLIT_MAX_B * (SPLIT_SLICES / SPLIT_MAX_B) <= SPLIT_SLICES && 4 * 64 <= SPLIT_SLICES &&
+              SPLIT_SLICES / 5 <= 64, "B * G <= SPLIT_SLICES and G <= 64 (one header per lane)");
+
+template <typename TIn>
+__global__ __launch_bounds__(NT, 1) void k_slices(Params p, uint32_t* hdr_all, uint32_t* ent_all)
+{
+    __shared__ uint32_t s_hist[2048], s_cs[64];
+    __shared__ uint32_t s_key[SLICE_CAP], s_id[SLICE_CAP];
+    __shared__ uint32_t s_n;
+    const int tid = threadIdx.x, lane = lane_id();
+    const int G = (int)gridDim.x, g = (int)blockIdx.x, r = (int)blockIdx.y;
+    const int V = p.V;
+    const TIn* rowp = (const TIn*)p.logits + (size_t)r * (size_t)p.ld;
+    uint32_t* hdr = hdr_all + (size_t)(r * G + g) * SL_HDR;
+    uint32_t* ent = ent_all + (size_t)(r * G + g) * SLICE_CAP * 2;
+    const float T = p.T[r];
+    const int k = p.K[r];
+    const float pen = p.PEN[r];
+    const int h0 = p.hoff ? p.hoff[r] : 0;
+    const int h1 = p.hoff ? (p.hend ? p.hend[r] : p.hoff[r + 1]) : 0;
+    const RowMode mode = classify(T, k, V);
+    const bool neg = T < 0.0f;
+    const bool pen_on = (pen != 1.0f) && (h1 > h0);
+    const bool defer = pen_on && !neg && pen >= 1.0f && pen <= 3.402823466e38f;
+    const bool topk = mode == MODE_TOPK && V >= FAST_MIN_V && (!pen_on || defer);
+    const bool greedy = mode == MODE_GREEDY && !pen_on;
+    if (!topk && !greedy) {
+        if (tid == 0) hdr[0] = SL_NONE;
+        return;
+    }
+    // the slice: whole multiples of 8 logits (16-byte vectors of either dtype)
+    const int L = (((V + G - 1) / G) + 7) & ~7;
+    const int s0 = g * L < V ? g * L : V;
+    const int n = (s0 + L < V ? s0 + L : V) - s0;
+    if (greedy) {   // sampling.py:47-48: the slice's first maximum
+        uint32_t bk = 0, bi = 0;
+        RowStream<TIn> rs(rowp + s0, n);
+        rs.template run<false>(nullptr, 1.0f,
+            [&](int, int e, float x) {
+                const uint32_t gk = (x != x) ? 0xFFFFFFFFu : vkey(x);   // NaN is the maximum
+                if (gk > bk) { bk = gk; bi = (uint32_t)(s0 + e); }
+            },
+            [&](auto&&) { return false; });
+        const u64 best = block_max<u64>(bk ? (((u64)bk << 32) | (u64)(0xFFFFFFFFu - bi)) : 0ull);
+        if (tid == 0) { hdr[5] = (uint32_t)best; hdr[6] = (uint32_t)(best >> 32); hdr[0] = 0; }
+        return;
+    }
+    constexpr int NS = NSAMP / NT;
+    float sx[NS];
+    const int se0 = (((tid >> 3) * (V >> 6)) & ~31) + (tid & 7) * NS;   // (the sample of k_fused)
+#pragma unroll
+    for (int q = 0; q < NS; ++q) sx[q] = VecIO<TIn>::one(rowp, se0 + q < V ? se0 + q : V - 1);
+    for (int b = tid; b < 2048; b += NT) s_hist[b] = 0;
+    if (tid < 64) s_cs[tid] = 0;
+    if (tid == 0) s_n = 0;
+    uint32_t est, theta;
+    sample_bound(sx, se0, (uint32_t)k, V, T, neg, false, pen, nullptr, s_hist, s_cs, est, theta);
+    // sampling.py:52-54: the slice's keys that reach the bound (raw keys: a
+    // deferred penalty never raises one), appended with one LDS atomic per
+    // wave and tile
+    uint32_t omax = 0, omin = 0xFFFFFFFFu, hm = 0;
+    uint32_t tk[FPT];
+    RowStream<TIn> rs(rowp + s0, n);
+    rs.template run<false>(nullptr, 1.0f,
+        [&](int i, int, float x) {
+            const uint32_t sk = selkey(x, neg);
+            omax = sk > omax ? sk : omax;
+            omin = sk < omin ? sk : omin;
+            tk[i] = sk;
+            hm |= (sk >= theta ? 1u : 0u) << i;
+        },
+        [&](auto&& id) -> bool {
+            const uint32_t c = (uint32_t)__builtin_popcount(hm);
+            const uint32_t incl = wave_prefix_u32(c);
+            const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+            if (tot) {
+                uint32_t base = 0;
+                if (lane == 63) base = atomicAdd(&s_n, tot);
+                uint32_t o = (uint32_t)__builtin_amdgcn_readlane((int)base, 63) + incl - c;
+#pragma unroll
+                for (int i = 0; i < FPT; ++i) {
+                    if ((hm >> i) & 1u) {
+                        if (o < (uint32_t)SLICE_CAP) { s_key[o] = tk[i]; s_id[o] = (uint32_t)(s0 + id(i)); }
+                        ++o;
+                    }
+                }
+            }
+            hm = 0;
+            return false;
+        });
+    const Reduced rd = block_reduce(omax, omin, 0u);   // (its barriers publish the list)
+    const uint32_t nh = s_n;
+    if (nh <= (uint32_t)SLICE_CAP)
+        for (uint32_t j = (uint32_t)tid; j < nh; j += NT) { ent[2 * j] = s_key[j]; ent[2 * j + 1] = s_id[j]; }
+    if (tid == 0) {
+        hdr[0] = nh <= (uint32_t)SLICE_CAP ? nh : SL_NONE;
+        hdr[1] = rd.max;
+        hdr[2] = rd.min;
+        hdr[3] = est;
+        hdr[4] = theta;
+    }
+}
+
 // Rows that finish_counts serves: fp16, top-k off, long, a temperature
 // that keeps every tempered value distinct and normal, and a finite positive
 // penalty whose history fits the list.
@@ -2059,7 +2234,9 @@ __device__ __forceinline__ bool finish_counts_as(const Params& p, int r, RowStre
     }
 }
 
-template <typename TIn>
+// SPLIT: the launch follows k_slices (small batches), whose candidates may
+// replace a row's stream; the instance without it has none of that code.
+template <typename TIn, bool SPLIT>
 __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
 {
     extern __shared__ __align__(16) unsigned char smem[];
@@ -2095,6 +2272,9 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
     pa = (lane == 5 && p.hoff) ? (const uint32_t*)(p.hend ? p.hend + r : p.hoff + r + 1) : pa;
     pa = (lane == 6 && p.U) ? (const uint32_t*)(p.U + r) : pa;
     const uint32_t pv = *pa;
+    // k_slices' slice headers of this row (a slice count per lane)
+    uint32_t sln = 0;
+    if constexpr (SPLIT) sln = p.sl_hdr[(size_t)(r * p.G + (lane < p.G ? lane : 0)) * SL_HDR];
     // The sample: NSAMP logits in 64 groups of 32 consecutive ones spread
     // over the row (a group is one 128-byte line of an fp32 row), 4 per
     // thread.  It is requested before the row's mode is known, so that it
@@ -2105,7 +2285,7 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
     const int se0 = (((tid >> 3) * (V >> 6)) & ~31) + (tid & 7) * NS;   // this thread's first sample
 #pragma unroll
     for (int q = 0; q < NS; ++q) sx[q] = VecIO<TIn>::one(rowp, se0 + q < V ? se0 + q : V - 1);
-    RowStream<TIn> rs(rowp, V);
+    RowStream<TIn> rs(rowp, V, !SPLIT);   // (after k_slices: only for rows it did not take)
     __builtin_amdgcn_sched_barrier(0);   // (the loads above stay ahead of the reads below)
     const float T = __builtin_bit_cast(float, (uint32_t)__builtin_amdgcn_readlane((int)pv, 0));
     const int k = __builtin_amdgcn_readlane((int)pv, 1);
@@ -2118,6 +2298,12 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
     const int h1 = p.hoff ? hv1 : 0;
     const float u = p.U ? uv : 0.0f;
     RowMode mode = classify(T, k, V);
+    // every slice of the row handed over its part: the candidates replace the stream
+    bool split = false;
+    if constexpr (SPLIT) {
+        split = !__ballot(lane < p.G && sln == SL_NONE);
+        if (!split) rs.restart();
+    }
     const bool neg = T < 0.0f;
     const bool pen_on = (pen != 1.0f) && (h1 > h0);
     int64_t tok = -1;
@@ -2286,7 +2472,12 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
         auto gkey = [](float x) -> uint32_t { return (x != x) ? 0xFFFFFFFFu : vkey(x); };   // NaN is the maximum
         u64 best = 0;
         uint32_t kmin;
-        bool have = raw_ok && raw_extremes(gkey, best, kmin);
+        bool have = split || (raw_ok && raw_extremes(gkey, best, kmin));
+        if (split) {   // the slices' maxima
+            const uint32_t* h = p.sl_hdr + (size_t)(r * p.G + (lane < p.G ? lane : 0)) * SL_HDR;
+            const u64 sb = lane < p.G ? (((u64)h[6] << 32) | h[5]) : 0ull;
+            best = wave_max<u64>(sb);
+        }
         if (!have) {
             if (raw_ok) rs.restart();
             uint32_t bk = 0, bi = 0;
@@ -2339,35 +2530,12 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
             //    k * NSAMP / V.  It only steers the stream; step 3 checks it.
             bool fast = sampled;
             if (tid == 0) s_ovf = 0u;
-            if (fast) {
-                uint32_t sk4[NS], smax = 0, smin = 0xFFFFFFFFu;
-#pragma unroll
-                for (int q = 0; q < NS; ++q) {
-                    const int e = se0 + q;   // (< V: rows that sample are long)
-                    float x = sx[q];
-                    if (pen_on && !defer && ((bm[e >> 5] >> (e & 31)) & 1u)) x = penalize(x, pen);
-                    sk4[q] = selkey(x, neg);
-                    smax = sk4[q] > smax ? sk4[q] : smax;
-                    smin = sk4[q] < smin ? sk4[q] : smin;
-                }
-                const float ks = (float)kk * (float)NSAMP / (float)V;
-                uint32_t js = (uint32_t)ceilf(ks + 6.0f * sqrtf(ks) + 3.0f);
-                js = js < (uint32_t)NSAMP ? js : (uint32_t)NSAMP;
-                const Reduced sr = block_reduce(smax, smin, 0u);   // (its barriers also order the zeroed hist)
-                const uint32_t span = sr.max - sr.min;
-                const int sh = span >= 2048u ? (32 - __builtin_clz(span)) - 11 : 0;
-#pragma unroll
-                for (int q = 0; q < NS; ++q) {
-                    const uint32_t b = (sk4[q] - sr.min) >> sh;
-                    atomicAdd(&hist[b], 1u);
-                    atomicAdd(&s_cs[b >> 5], 1u);
-                }
-                __syncthreads();
-                // (every wave finds the bin by itself)
-                const WHit hb = wave_find_desc<uint32_t>(hist, (u64)s_cs[lane], (u64)(js - 1u));
-                est = sr.min + ((uint32_t)hb.bin << sh);
-                if (est < SK_MIN) est = SK_MIN;
-                theta = widen_threshold(est, T, neg);
+            if (fast && split) {   // k_slices computed the same bound
+                est = p.sl_hdr[(size_t)r * p.G * SL_HDR + 3];
+                theta = p.sl_hdr[(size_t)r * p.G * SL_HDR + 4];
+                __syncthreads();   // (s_ovf is cleared before any wave may set it)
+            } else if (fast) {
+                sample_bound(sx, se0, kk, V, T, neg, pen_on && !defer, pen, bm, hist, s_cs, est, theta);
             }
             if (fast) {
                 // 2. The stream: each wave appends its hits to its own segment
@@ -2384,36 +2552,81 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                 uint32_t tk[FPT];   // this tile's keys
                 uint32_t hm = 0;    // this lane's hits in the tile, one bit per slot
                 constexpr uint32_t SEG_USE = FSEG - 64;   // [SEG_USE, FSEG): the dummy words
-                rs.run_pen(bm, pen_on && !defer, pen,
-                    [&](int i, int, float x) {
-                        const uint32_t sk = selkey(x, neg);
-                        omax = sk > omax ? sk : omax;
-                        omin = sk < omin ? sk : omin;
-                        tk[i] = sk;
-                        hm |= (sk >= theta ? 1u : 0u) << i;
-                    },
-                    [&](auto&& id) -> bool {
-                        const uint32_t c = (uint32_t)__builtin_popcount(hm);
-                        const uint32_t incl = wave_prefix_u32(c);
-                        const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
-                        if (cw + tot > SEG_USE) {
-                            if (lane == 0) __hip_atomic_store(&s_ovf, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                            return true;
-                        }
-                        uint32_t o = cw + incl - c;
-                        const uint32_t dummy = SEG_USE + (uint32_t)lane;
+                if (split) {
+                    // the candidates of slices w, w + NWAVES, ... into this wave's
+                    // segment: the slices' headers one per lane, their offsets by
+                    // a wave prefix, then the entries eight loads per lane at a
+                    // time (clamped indices: no load behind a branch)
+                    const int nsw = w < p.G ? (p.G - w + NWAVES - 1) / NWAVES : 0;   // (<= 64 / NWAVES)
+                    const int gh = w + NWAVES * (lane < nsw ? lane : 0);   // (a wave without slices reads slice G - 1)
+                    const uint32_t* h = p.sl_hdr + (size_t)(r * p.G + (gh < p.G ? gh : p.G - 1)) * SL_HDR;
+                    const bool mine = lane < nsw;
+                    const uint32_t hn = h[0], hmx = h[1], hmn = h[2];
+                    const uint32_t ng = mine ? hn : 0u;
+                    omax = wave_max_u32(mine ? hmx : 0u);
+                    omin = wave_min_u32(mine ? hmn : 0xFFFFFFFFu);
+                    const uint32_t incl = wave_prefix_u32(ng);
+                    const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+                    const uint32_t excl = incl - ng;
+                    if (total > SEG_USE) {
+                        if (lane == 0) __hip_atomic_store(&s_ovf, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                    } else {
+                        for (uint32_t q0 = 0; q0 < total; q0 += 512u) {
+                            uint2 v[8];
 #pragma unroll
-                        for (int i = 0; i < FPT; ++i) {
-                            const uint32_t h = (hm >> i) & 1u;
-                            const uint32_t a = h ? o : dummy;
-                            wck[a] = tk[i];
-                            wci[a] = (uint32_t)id(i);
-                            o += h;
+                            for (int i = 0; i < 8; ++i) {
+                                uint32_t q = q0 + (uint32_t)lane + 64u * (uint32_t)i;
+                                q = q < total ? q : total - 1u;
+                                // the slice holding position q: the last one that starts at or below it
+                                int ls = 0;
+                                uint32_t base = 0;
+                                for (int l = 1; l < nsw; ++l) {
+                                    const uint32_t el = (uint32_t)__builtin_amdgcn_readlane((int)excl, l);
+                                    if (q >= el) { ls = l; base = el; }
+                                }
+                                const uint2* e = (const uint2*)(p.sl_ent + (size_t)(r * p.G + w + NWAVES * ls) * SLICE_CAP * 2);
+                                v[i] = e[q - base];
+                            }
+#pragma unroll
+                            for (int i = 0; i < 8; ++i) {
+                                const uint32_t q = q0 + (uint32_t)lane + 64u * (uint32_t)i;
+                                if (q < total) { wck[q] = v[i].x; wci[q] = v[i].y; }
+                            }
                         }
-                        hm = 0;
-                        cw += tot;
-                        return __hip_atomic_load(&s_ovf, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0u;
-                    });
+                        cw = total;
+                    }
+                } else {
+                    rs.run_pen(bm, pen_on && !defer, pen,
+                        [&](int i, int, float x) {
+                            const uint32_t sk = selkey(x, neg);
+                            omax = sk > omax ? sk : omax;
+                            omin = sk < omin ? sk : omin;
+                            tk[i] = sk;
+                            hm |= (sk >= theta ? 1u : 0u) << i;
+                        },
+                        [&](auto&& id) -> bool {
+                            const uint32_t c = (uint32_t)__builtin_popcount(hm);
+                            const uint32_t incl = wave_prefix_u32(c);
+                            const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+                            if (cw + tot > SEG_USE) {
+                                if (lane == 0) __hip_atomic_store(&s_ovf, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                                return true;
+                            }
+                            uint32_t o = cw + incl - c;
+                            const uint32_t dummy = SEG_USE + (uint32_t)lane;
+#pragma unroll
+                            for (int i = 0; i < FPT; ++i) {
+                                const uint32_t h = (hm >> i) & 1u;
+                                const uint32_t a = h ? o : dummy;
+                                wck[a] = tk[i];
+                                wci[a] = (uint32_t)id(i);
+                                o += h;
+                            }
+                            hm = 0;
+                            cw += tot;
+                            return __hip_atomic_load(&s_ovf, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0u;
+                        });
+                }
                 if (lane == 0) s_seg[w] = cw;
                 bool bad = false;
                 if (late_bm) bad = build_bitmap();
@@ -2728,17 +2941,31 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
     }
 }
 
-// The workspace of the C ABI: every kernel here keeps a row's state in LDS,
-// so a call needs only this token amount.
-constexpr size_t WORKSPACE_BYTES = 256;
+// The workspace of the C ABI: k_fused keeps a row's state in LDS; the
+// workspace holds what k_slices hands over for batches of up to SPLIT_MAX_B
+// rows (the same size for every batch, so that a buffer sized once serves
+// every batch).
+constexpr size_t WORKSPACE_BYTES = (SL_WS_BYTES + 255) & ~(size_t)255;
 
+// k_slices first when the batch is small (p.sl_hdr set), then k_fused.
 template <typename TIn>
 hipError_t launch(const Params& p, hipStream_t s)
 {
-    static const hipError_t a0 = hipFuncSetAttribute((const void*)k_fused<TIn>,
+    static const hipError_t a0 = hipFuncSetAttribute((const void*)k_fused<TIn, false>,
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, KF_LDS_BYTES);
+    static const hipError_t a1 = hipFuncSetAttribute((const void*)k_fused<TIn, true>,
                                                      hipFuncAttributeMaxDynamicSharedMemorySize, KF_LDS_BYTES);
     (void)a0;
-    hipLaunchKernelGGL(k_fused<TIn>, dim3((unsigned)p.B), dim3(NT), KF_LDS_BYTES, s, p);
+    (void)a1;
+    if (p.sl_hdr) {
+        hipLaunchKernelGGL(k_slices<TIn>, dim3((unsigned)p.G, (unsigned)p.B), dim3(NT), 0, s, p,
+                           (uint32_t*)p.sl_hdr, (uint32_t*)p.sl_ent);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL((k_fused<TIn, true>), dim3((unsigned)p.B), dim3(NT), KF_LDS_BYTES, s, p);
+    } else {
+        hipLaunchKernelGGL((k_fused<TIn, false>), dim3((unsigned)p.B), dim3(NT), KF_LDS_BYTES, s, p);
+    }
     return hipGetLastError();
 }
 
@@ -2810,7 +3037,15 @@ int sample_impl(const void* logits, int dtype, int B, int V, int64_t ld,
     p.out_status = out_status;
     p.out_probs = out_probs;
 
+    p.sl_hdr = nullptr;
+    p.sl_ent = nullptr;
+    p.G = 0;
     hipStream_t s = (hipStream_t)stream;
+    if (B <= SPLIT_MAX_B) {
+        p.G = split_slices(B);
+        p.sl_hdr = (const uint32_t*)workspace;
+        p.sl_ent = (const uint32_t*)((const char*)workspace + SL_HDR_BYTES);
+    }
     hipError_t e = dtype == MXS_DTYPE_F32 ? launch<float>(p, s) : launch<__half>(p, s);
     return e == hipSuccess ? MXS_OK : MXS_ERR_HIP;
 }
