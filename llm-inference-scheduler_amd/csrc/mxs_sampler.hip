@@ -1400,29 +1400,28 @@ __device__ __forceinline__ bool finish_wide(const Params& p, int r, float T, boo
     };
     auto is_history = [&](int e) { return ((bm[e >> 5] >> (e & 31)) & 1u) != 0u; };
 
-    // sampling.py:57-59: every element's mass, histogrammed by bin
-    for (int b = tid; b < 2048; b += NT) { MH[b] = 0; CH[b] = 0; }
+    // sampling.py:57-59: every element's mass, histogrammed by bin (masses
+    // without branches: count_mass(1, d) is mass_of(d) for d <= 0, and the
+    // raw value of a history id, which may lie above m, is taken out again
+    // with the same function below)
+    for (int b = tid; b < 2048; b += NT) MH[b] = 0;
     __syncthreads();
     u64 wsum = 0;
     stream_row<TIn, false>(rowp, V, bm, pen,
         [&](int, int, float x) {
             const float l = x / T;
             const float d = l - m;
-            const u64 w = mass_of(d);
-            const uint32_t b = bin_of(d);
-            atomicAdd(&MH[b], w);
-            atomicAdd(&CH[b], 1u);
+            const u64 w = count_mass(1u, d);
+            atomicAdd(&MH[bin_of(d)], w);
             wsum += w;
         },
         [&](auto&&) { return false; });
     if (pen_on) {   // the history ids: raw contribution out, penalized one in
         for_history([&](int, float x) {
             const float d0 = x / T - m, d1 = penalize(x, pen) / T - m;
-            const u64 w0 = mass_of(d0), w1 = mass_of(d1);
+            const u64 w0 = count_mass(1u, d0), w1 = count_mass(1u, d1);
             atomicAdd(&MH[bin_of(d0)], 0ull - w0);
-            atomicAdd(&CH[bin_of(d0)], 0xFFFFFFFFu);
             atomicAdd(&MH[bin_of(d1)], w1);
-            atomicAdd(&CH[bin_of(d1)], 1u);
             wsum += w1 - w0;
         });
     }
@@ -1490,7 +1489,6 @@ __device__ __forceinline__ bool finish_wide(const Params& p, int r, float T, boo
             const BinHit h2 = find_desc<u64>(MH, 2048, Dhi);
             if (h1.bin == h2.bin) bd = h1.bin;
         }
-        if (CH[hc.bin] > (uint32_t)LCAP || (bd >= 0 && CH[bd] > (uint32_t)LCAP)) return false;
         if (!gather(hc.bin, bd)) return false;
         const int nc = (int)g_cnt[0], nd = (int)g_cnt[1];
         const SetPick c = pick_in_set(keys_c, nc, t - A, m, SMH, SCH);
@@ -1504,7 +1502,6 @@ __device__ __forceinline__ bool finish_wide(const Params& p, int r, float T, boo
         } else {
             const BinHit hd = find_desc<u64>(MH, 2048, D);   // a bin above the cut's, wholly kept
             if (hd.bin != bd) {
-                if (CH[hd.bin] > (uint32_t)LCAP) return false;
                 if (!gather(hd.bin, -1)) return false;
                 dp = pick_in_set(keys_c, (int)g_cnt[0], D - hd.above, m, SMH, SCH);
             } else {
@@ -1514,7 +1511,6 @@ __device__ __forceinline__ bool finish_wide(const Params& p, int r, float T, boo
     } else {
         const u64 D = floor_mul(clamp_uniform(u), W);   // sampling.py:69
         const BinHit hd = find_desc<u64>(MH, 2048, D);
-        if (CH[hd.bin] > (uint32_t)LCAP) return false;
         if (!gather(hd.bin, -1)) return false;
         dp = pick_in_set(keys_c, (int)g_cnt[0], D - hd.above, m, SMH, SCH);
     }
