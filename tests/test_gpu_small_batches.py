@@ -1,0 +1,79 @@
+"""Batches of up to 64 rows go through k_slices (each top-k row with a
+deferrable penalty, and each greedy row without one, cut into up to 64
+slices that hand their candidates over) before k_fused.  Cases where the
+hand-over must give way: a slice with more candidates than it can hold,
+a bound that fails (heavy ties), NaN inside one slice, rows it does not take
+(penalty below 1, T < 0, top-k off, k above the candidate cap), odd vocab
+sizes whose last slices are short or empty, and unaligned fp16 rows.
+"""
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from mi355x_sampler import sample_batch
+from mi355x_sampler.workloads import VOCAB, Workload
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def batch(B, V, seed, dtype=np.float32):
+    rng = np.random.default_rng(seed)
+    x = (2.0 * rng.standard_normal((B, V))).astype(np.float32)
+    T = np.full(B, 0.8, np.float32)
+    k = rng.integers(1, 1025, B).astype(np.int32)
+    p = rng.uniform(0.5, 1.0, B).astype(np.float32)
+    pen = np.where(rng.random(B) < 0.5, 1.0, rng.uniform(1.0, 1.3, B)).astype(np.float32)
+    for r in range(B):
+        c = r % 9
+        if c == 1:     # greedy, no penalty
+            T[r] = 0.0; pen[r] = 1.0
+        elif c == 2:   # heavy ties: more candidates than a slice holds, or a failed bound
+            x[r] = rng.integers(0, 3, V).astype(np.float32); k[r] = 1000
+        elif c == 3:   # NaN inside one slice
+            x[r, int(rng.integers(0, V))] = np.nan; T[r] = 0.0 if r % 2 else 0.9; pen[r] = 1.0
+        elif c == 4:   # penalty below 1: not taken
+            pen[r] = 0.7
+        elif c == 5:   # T < 0: not taken
+            T[r] = -0.9
+        elif c == 6:   # top-k off: not taken
+            k[r] = 0
+        elif c == 7:   # k above the candidate cap: not taken
+            k[r] = 3000
+        elif c == 8:   # the row's maximum is a history id
+            pass
+    hists = []
+    for r in range(B):
+        h = rng.integers(0, V, 300)
+        if r % 9 == 8:
+            h[:3] = np.argsort(-np.nan_to_num(x[r], nan=-np.inf))[:3]
+        hists.append(h.astype(np.int32))
+    off = np.zeros(B + 1, np.int32)
+    off[1:] = np.cumsum([len(h) for h in hists])
+    u = rng.random(B).astype(np.float32)
+    return Workload(f"small{B}", x.astype(dtype), T, k, p, pen, off, np.concatenate(hists), u)
+
+
+@pytest.mark.parametrize("B,V,dtype", [(1, VOCAB, np.float32), (3, VOCAB, np.float32), (5, 40001, np.float16),
+                                       (17, 65536, np.float32), (64, VOCAB, np.float16), (9, 16384, np.float32),
+                                       (2, 16391, np.float16)])
+def test_split_batches_match_the_oracle(oracle, cuda, B, V, dtype):
+    for seed in (1, 2):
+        w = batch(B, V, seed, dtype)
+        say(f"[small] B={B} V={V} {np.dtype(dtype).name} seed={seed}")
+        ref = oracle.sample_rows(w.logits, w.temperature, w.top_k, w.top_p, w.penalty,
+                                 w.hist_offsets, w.hist_ids, w.uniforms, want_probs=True)
+        d = w.to_device(cuda)
+        probs = torch.zeros((B, V), dtype=torch.float32, device=cuda)
+        tok, st = sample_batch(**d, out_probs=probs, return_status=True)
+        torch.cuda.synchronize()
+        assert np.array_equal(st.cpu().numpy(), ref.status)
+        assert np.array_equal(tok.cpu().numpy(), ref.tokens), (tok.cpu().numpy(), ref.tokens)
+        assert np.abs(probs.cpu().numpy() - ref.probs).max() <= 1e-6
