@@ -1055,8 +1055,11 @@ struct RowStream {
             b[j] = src[vi < lastv ? vi : lastv];
         }
     }
-    // PART: the last tile, which may end inside the row's vectors
-    template <bool PART, bool PEN, class Elem>
+    // PART: the last tile, which may end inside the row's vectors.  ALL:
+    // every slot is visited, elem(i, e, x, valid), so that no lane leaves the
+    // others (a slot past the row's end has valid false and x a duplicate of
+    // one of the row's values).
+    template <bool PART, bool PEN, bool ALL, class Elem>
     __device__ __forceinline__ void proc(const vec_t (&b)[FU], int t, const uint32_t* bm, float pen, Elem& elem)
     {
         const int tid = threadIdx.x;
@@ -1071,7 +1074,7 @@ struct RowStream {
 #pragma unroll
         for (int j = 0; j < FU; ++j) {
             const int vi = t * TV + j * NT + tid;
-            if (PART && vi >= nvec) continue;
+            if (!ALL && PART && vi >= nvec) continue;
             float xs[VW];
             IO::unpack(b[j], xs);
             const int e = vi * VW;
@@ -1083,11 +1086,17 @@ struct RowStream {
                         if ((bits >> q) & 1u) xs[q] = penalize(xs[q], pen);
                 }
             }
+            if constexpr (ALL) {
+                const bool valid = !PART || vi < nvec;
 #pragma unroll
-            for (int q = 0; q < VW; ++q) elem(j * VW + q, e + q, xs[q]);
+                for (int q = 0; q < VW; ++q) elem(j * VW + q, e + q, xs[q], valid);
+            } else {
+#pragma unroll
+                for (int q = 0; q < VW; ++q) elem(j * VW + q, e + q, xs[q]);
+            }
         }
     }
-    template <bool PEN, class Elem, class TileEnd>
+    template <bool PEN, bool ALL = false, class Elem, class TileEnd>
     __device__ __forceinline__ void run(const uint32_t* bm, float pen, Elem&& elem, TileEnd&& tile_end)
     {
         const int tid = threadIdx.x;
@@ -1098,22 +1107,22 @@ struct RowStream {
         // A holds tile t, Bf tile t + 1
         int t = 0;
         for (; t + 1 < nfull; t += 2) {
-            proc<false, PEN>(A, t, bm, pen, elem);
+            proc<false, PEN, ALL>(A, t, bm, pen, elem);
             if (tile_end(vid(t))) return;
             load(A, t + 2);
-            proc<false, PEN>(Bf, t + 1, bm, pen, elem);
+            proc<false, PEN, ALL>(Bf, t + 1, bm, pen, elem);
             if (tile_end(vid(t + 1))) return;
             load(Bf, t + 3);
         }
         if (t < nfull) {
-            proc<false, PEN>(A, t, bm, pen, elem);
+            proc<false, PEN, ALL>(A, t, bm, pen, elem);
             if (tile_end(vid(t))) return;
             ++t;
 #pragma unroll
             for (int j = 0; j < FU; ++j) A[j] = Bf[j];   // (one call site for the last tile)
         }
         if (t < ntile) {
-            proc<true, PEN>(A, t, bm, pen, elem);
+            proc<true, PEN, ALL>(A, t, bm, pen, elem);
             if (tile_end(vid(t))) return;
         }
         // the rest of the row (all of a row that is not 16-byte aligned), element by element
@@ -1122,17 +1131,19 @@ struct RowStream {
 #pragma unroll
             for (int i = 0; i < FPT; ++i) {
                 const int e = e0 + i * NT + tid;
-                xs[i] = e < V ? IO::one(rowp, e) : 0.0f;
+                xs[i] = ALL ? IO::one(rowp, e < V ? e : V - 1) : (e < V ? IO::one(rowp, e) : 0.0f);
             }
 #pragma unroll
             for (int i = 0; i < FPT; ++i) {
                 const int e = e0 + i * NT + tid;
-                if (e < V) {
+                if (ALL || e < V) {
+                    const int ev = e < V ? e : V - 1;
                     float x = xs[i];
                     if constexpr (PEN) {
-                        if ((bm[e >> 5] >> (e & 31)) & 1u) x = penalize(x, pen);
+                        if ((bm[ev >> 5] >> (ev & 31)) & 1u) x = penalize(x, pen);
                     }
-                    elem(i, e, x);
+                    if constexpr (ALL) elem(i, e, x, e < V);
+                    else elem(i, e, x);
                 }
             }
             if (tile_end([=](int i) { return e0 + i * NT + tid; })) return;
@@ -1145,6 +1156,14 @@ struct RowStream {
     {
         if (pen_inline) run<true>(bm, pen, elem, tile_end);
         else run<false>(bm, pen, elem, tile_end);
+    }
+    // run_pen() visiting every slot: elem(i, e, x, valid)
+    template <class Elem, class TileEnd>
+    __device__ __forceinline__ void run_pen_all(const uint32_t* bm, bool pen_inline, float pen, Elem&& elem,
+                                                TileEnd&& tile_end)
+    {
+        if (pen_inline) run<true, true>(bm, pen, elem, tile_end);
+        else run<false, true>(bm, pen, elem, tile_end);
     }
     // One pass over the raw 16-bit values of an fp16 row: vec(v, e) for each
     // whole vector (elements e .. e + 7, two per 32-bit word), then
@@ -2322,6 +2341,7 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");   // before the writes of the kept probabilities
     }
     if (tid < 3) s_cnt[tid] = 0;
+    if (tid == 0) s_ovf = 0u;   // (a barrier follows before any wave may set it)
 
     // sampling.py:38-45: the row's history ids, each once (sorted(set())).
     // The first HB per thread are requested now and held in registers.
@@ -2386,6 +2406,16 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
         if (block_max<uint32_t>(build_bitmap() ? 1u : 0u)) st = MXS_ROW_BAD_HISTORY;   // (its barriers publish bm)
     }
     if (st == MXS_ROW_OK && mode == MODE_INVALID) st = MXS_ROW_BAD_PARAM;
+
+    // A top-k row's first bound (step 1 below) is taken here, on the straight
+    // path from the kernel's entry: at a join of the row modes' paths the
+    // compiler's wait for the sample would also wait for the first tiles
+    // (other paths leave loads pending into the same registers), which held
+    // every row for the tiles' arrival.  (A row with an error computes it too;
+    // nothing reads it then.)
+    uint32_t est0 = 0, theta0 = 0;
+    if (sampled && !split)
+        sample_bound(sx, se0, (uint32_t)k, V, T, neg, pen_on && !defer, pen, bm, hist, s_cs, est0, theta0);
 
     // The penalized row's extremes from a raw stream (no penalty branch per
     // element): key_of(x) ranks a value; best gets the packed maximum
@@ -2524,14 +2554,15 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
             //    sample of NSAMP logits: the lower edge of the histogram bin
             //    holding the sample's j-th largest, j well above the expected
             //    k * NSAMP / V.  It only steers the stream; step 3 checks it.
+            //    (Computed before the row modes branch, as est0 / theta0.)
             bool fast = sampled;
-            if (tid == 0) s_ovf = 0u;
             if (fast && split) {   // k_slices computed the same bound
                 est = p.sl_hdr[(size_t)r * p.G * SL_HDR + 3];
                 theta = p.sl_hdr[(size_t)r * p.G * SL_HDR + 4];
                 __syncthreads();   // (s_ovf is cleared before any wave may set it)
             } else if (fast) {
-                sample_bound(sx, se0, kk, V, T, neg, pen_on && !defer, pen, bm, hist, s_cs, est, theta);
+                est = est0;
+                theta = theta0;
             }
             if (fast) {
                 // 2. The stream: each wave appends its hits to its own segment
@@ -2540,14 +2571,8 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                 const int w = wave_id();
                 uint32_t* wck = ck + w * FSEG;
                 uint32_t* wci = ci + w * FSEG;
-                uint32_t cw = 0;
-                // Each lane appends its own hits in slot order at its offset
-                // in the wave's segment (an exclusive prefix of the lanes' hit
-                // counts); a slot without a hit writes a per-lane dummy word
-                // at the segment's end instead, so the appends need no branch.
-                uint32_t tk[FPT];   // this tile's keys
-                uint32_t hm = 0;    // this lane's hits in the tile, one bit per slot
-                constexpr uint32_t SEG_USE = FSEG - 64;   // [SEG_USE, FSEG): the dummy words
+                uint32_t cw = 0;   // (wave-uniform) entries in this wave's segment
+                constexpr uint32_t SEG_USE = FSEG - 64;   // a segment's room
                 if (split) {
                     // the candidates of slices w, w + NWAVES, ... into this wave's
                     // segment: the slices' headers one per lane, their offsets by
@@ -2592,36 +2617,64 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                         cw = total;
                     }
                 } else {
-                    rs.run_pen(bm, pen_on && !defer, pen,
-                        [&](int i, int, float x) {
-                            const uint32_t sk = selkey(x, neg);
-                            omax = sk > omax ? sk : omax;
-                            omin = sk < omin ? sk : omin;
-                            tk[i] = sk;
-                            hm |= (sk >= theta ? 1u : 0u) << i;
-                        },
-                        [&](auto&& id) -> bool {
-                            const uint32_t c = (uint32_t)__builtin_popcount(hm);
-                            const uint32_t incl = wave_prefix_u32(c);
-                            const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
-                            if (cw + tot > SEG_USE) {
-                                if (lane == 0) __hip_atomic_store(&s_ovf, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                                return true;
-                            }
-                            uint32_t o = cw + incl - c;
-                            const uint32_t dummy = SEG_USE + (uint32_t)lane;
+                    // A hit is tested on the value itself: x >= tf (x <= tf for
+                    // T < 0), tf the value of theta.  Every key >= theta passes;
+                    // the test adds at most a -0 against a bound of +0, which
+                    // widening never leaves (it goes below -0 then).  The
+                    // row's extremes are NaN-propagating maxima and minima of
+                    // the values, and the segments take the values' raw bits
+                    // (the count pass turns them into keys).  Each lane counts
+                    // its hits; at the tile's end one wave prefix gives each
+                    // lane its offset in the segment, and every slot is written
+                    // without a branch (a miss writes a per-lane dummy word at
+                    // the segment's end).  No barrier, no atomics.
+                    const float tf = sel_inv(theta, neg);
+                    float fmx = -INFINITY, fmn = INFINITY;
+                    float tx[FPT];      // this tile's values
+                    uint32_t nhit = 0;  // this lane's hits in the tile
+                    auto stream = [&](auto negc) {
+                        constexpr bool NEG = decltype(negc)::value;
+                        auto hit = [&](float x) { return NEG ? x <= tf : x >= tf; };
+                        // (every slot is visited: a slot past the row's end holds
+                        // NaN, never a hit, instead of the last tile's value)
+                        rs.run_pen_all(bm, pen_on && !defer, pen,
+                            [&](int i, int, float x, bool valid) {
+                                fmx = __builtin_elementwise_maximum(fmx, x);
+                                fmn = __builtin_elementwise_minimum(fmn, x);
+                                tx[i] = valid ? x : __builtin_nanf("");
+                                nhit += hit(tx[i]) ? 1u : 0u;
+                            },
+                            [&](auto&& id) -> bool {
+                                const uint32_t incl = wave_prefix_u32(nhit);
+                                const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+                                if (cw + tot > SEG_USE) {
+                                    if (lane == 0) __hip_atomic_store(&s_ovf, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                                    return true;
+                                }
+                                uint32_t o = cw + incl - nhit;
+                                const uint32_t dummy = SEG_USE + (uint32_t)lane;
 #pragma unroll
-                            for (int i = 0; i < FPT; ++i) {
-                                const uint32_t h = (hm >> i) & 1u;
-                                const uint32_t a = h ? o : dummy;
-                                wck[a] = tk[i];
-                                wci[a] = (uint32_t)id(i);
-                                o += h;
-                            }
-                            hm = 0;
-                            cw += tot;
-                            return __hip_atomic_load(&s_ovf, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0u;
-                        });
+                                for (int i = 0; i < FPT; ++i) {
+                                    const bool h = hit(tx[i]);
+                                    const uint32_t a = h ? o : dummy;
+                                    wck[a] = f2u(tx[i]);
+                                    wci[a] = (uint32_t)id(i);
+                                    o += h ? 1u : 0u;
+                                }
+                                nhit = 0;
+                                cw += tot;
+                                return __hip_atomic_load(&s_ovf, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0u;
+                            });
+                    };
+                    if (neg) stream(std::integral_constant<bool, true>{});
+                    else stream(std::integral_constant<bool, false>{});
+                    if (fmx != fmx) {   // a NaN (both extremes carry it): keys that say so
+                        omax = 0xFFFFFFFFu;
+                        omin = 0u;
+                    } else {
+                        omax = neg ? selkey(fmn, true) : selkey(fmx, false);
+                        omin = neg ? selkey(fmx, true) : selkey(fmn, false);
+                    }
                 }
                 if (lane == 0) s_seg[w] = cw;
                 bool bad = false;
@@ -2669,8 +2722,12 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                     for (int q = 0; q < 4; ++q) {
                         const uint32_t j = j0 + 64u * q;
                         if (j >= cw) continue;
-                        if ((bw[q] >> (id[q] & 31)) & 1u) {
-                            key[q] = okey(penalize(okey_inv(key[q]), pen));
+                        // (the stream left raw values; k_slices' candidates are keys)
+                        float x = split ? sel_inv(key[q], neg) : u2f(key[q]);
+                        const bool hp = (bw[q] >> (id[q] & 31)) & 1u;
+                        if (hp) x = penalize(x, pen);
+                        if (!split || hp) {
+                            key[q] = selkey(x, neg);
                             wck[j] = key[q];
                         }
                         cmx = key[q] > cmx ? key[q] : cmx;
