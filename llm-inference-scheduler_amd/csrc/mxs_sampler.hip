@@ -831,7 +831,7 @@ __device__ __forceinline__ bool finish_segs(const Params& p, int r, const uint32
     // (at least k elements are binned: the bound held)
     const int kb = g_kb;
     const uint32_t nabove = g_kabove, nkb = g_kn;
-    if (nabove + nkb > (uint32_t)KL_CAP || nkb > 64u) return false;
+    if (__builtin_expect(nabove + nkb > (uint32_t)KL_CAP || nkb > 64u, 0)) return false;
     // the bins from kb up: masses, and their places in KL
     const uint32_t tkb = (uint32_t)kb + 1u;
     // four entries per lane at a time: loads, then arithmetic, then the
@@ -956,7 +956,7 @@ __device__ __forceinline__ bool finish_segs(const Params& p, int r, const uint32
         }
     }
     __syncthreads();
-    if (g_fail) return false;
+    if (__builtin_expect(g_fail != 0, 0)) return false;
     st = g_st;
     if (st != MXS_ROW_OK) { tok = -1; return true; }
     tok = (int64_t)(0xFFFFFFFFu - (uint32_t)g_tok);
@@ -2647,7 +2647,7 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                             [&](auto&& id) -> bool {
                                 const uint32_t incl = wave_prefix_u32(nhit);
                                 const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
-                                if (cw + tot > SEG_USE) {
+                                if (__builtin_expect(cw + tot > SEG_USE, 0)) {
                                     if (lane == 0) __hip_atomic_store(&s_ovf, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
                                     return true;
                                 }
@@ -2761,7 +2761,7 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                 if (badw) st = MXS_ROW_BAD_HISTORY;
                 fast = st == MXS_ROW_OK && s_ovf == 0u && reach >= kk;
                 segs = fast;
-                if (segs && binned && cmax != rd.max) {
+                if (__builtin_expect(segs && binned && cmax != rd.max, 0)) {
                     // the penalty lowered the row's maximum: the bins and
                     // masses again, relative to the penalized maximum
                     m0 = sel_inv(cmax, neg) / T;
@@ -2785,7 +2785,7 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                     __syncthreads();
                 }
             }
-            if (!fast && st == MXS_ROW_OK) {
+            if (__builtin_expect(!fast && st == MXS_ROW_OK, 0)) {
                 // 4. The stream again with one shared buffer and a running
                 //    bound raised by compaction whenever it nears capacity.
                 theta = 0;
@@ -2896,7 +2896,7 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
         const bool has_inf = rd.max >= 0xFF800000u || rd.min <= 0x007FFFFFu;
         if (st != MXS_ROW_OK) {
             // a history id outside [0, V), found after the stream
-        } else if (has_nan || (has_inf && __builtin_isinf(T))) {
+        } else if (__builtin_expect(has_nan || (has_inf && __builtin_isinf(T)), 0)) {
             st = MXS_ROW_NONFINITE;   // a NaN tempered logit heads the order (sampling.py:57-58)
         } else {
             bool done = false;
@@ -2907,7 +2907,7 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                     // (its kept list goes where the history bitmap was)
                     done = finish_segs(p, r, ck, ci, s_seg, T, neg, kk, m0, top_p, u, MH, hist, s_ms,
                                        (u64*)(smem + KF_BM), tok, st);
-                    if (!done && pen_on) {   // the general path needs the bitmap again
+                    if (__builtin_expect(!done && pen_on, 0)) {   // the general path needs the bitmap again
                         const int words = (V + 31) >> 5;
                         for (int w2 = tid; w2 < words; w2 += NT) bm[w2] = 0;
                         __syncthreads();
@@ -2915,7 +2915,7 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                         __syncthreads();
                     }
                 }
-                if (!done) {
+                if (__builtin_expect(!done, 0)) {
                     // compact the segments (ids without their bin tags): the
                     // buffer becomes [0, Nc) for the general path
                     constexpr int PERW = FSEG / 64;
@@ -2941,7 +2941,7 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                     __syncthreads();
                 }
             }
-            if (mode == MODE_TOPK && !overflow && !done) {
+            if (__builtin_expect(mode == MODE_TOPK && !overflow && !done, 0)) {
                 auto visit = [&](auto&& f) {
                     for (uint32_t j = tid; j < Nc; j += NT) f(ck[j]);
                 };
@@ -2978,7 +2978,7 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                                         (u64*)(smem + KF_CK + 16 * LCAP),
                                         (uint32_t*)(smem + KF_CK + 16 * LCAP + 8 * 2048), tok, st);
             }
-            if (!done) {
+            if (__builtin_expect(!done, 0)) {
                 __syncthreads();
                 const LargeLds lds{bm, (u64*)(smem + KF_MH), (u64*)(smem + KF_CK), hist};
                 const uint32_t skmax = rd.max;
