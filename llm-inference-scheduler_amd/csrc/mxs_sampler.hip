@@ -2806,6 +2806,11 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                         hm |= (sk >= theta ? 1u : 0u) << i;
                     },
                     [&](auto&&) -> bool {
+                        // after massive ties the rest of the row is still
+                        // streamed, for its extremes (the row maximum and the
+                        // NaN and infinity tests need every element), but
+                        // nothing more is appended
+                        if (overflow) { hm = 0; return false; }
                         // append this tile's hits: one LDS atomic per wave
                         uint32_t wtot;
                         const uint32_t pre = wave_excl_small((uint32_t)__builtin_popcount(hm), wtot);
@@ -2867,7 +2872,7 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                         Nc = total;
                         Nfix = total;
                         __syncthreads();
-                        if (Nc > (uint32_t)(FCAP - FTILE)) { overflow = true; return true; }   // massive ties
+                        if (Nc > (uint32_t)(FCAP - FTILE)) overflow = true;   // massive ties
                         return false;
                     });
                 if (!overflow) fix_up();
