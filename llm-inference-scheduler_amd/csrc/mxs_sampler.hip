@@ -2572,7 +2572,7 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                 uint32_t* wck = ck + w * FSEG;
                 uint32_t* wci = ci + w * FSEG;
                 uint32_t cw = 0;   // (wave-uniform) entries in this wave's segment
-                constexpr uint32_t SEG_USE = FSEG - 64;   // a segment's room
+                constexpr uint32_t SEG_USE = FSEG - 64;   // [SEG_USE, FSEG): the dummy words
                 if (split) {
                     // the candidates of slices w, w + NWAVES, ... into this wave's
                     // segment: the slices' headers one per lane, their offsets by
@@ -2619,8 +2619,9 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                 } else {
                     // A hit is tested on the value itself: x >= tf (x <= tf for
                     // T < 0), tf the value of theta.  Every key >= theta passes;
-                    // the test adds at most a -0 against a bound of +0, which
-                    // widening never leaves (it goes below -0 then).  The
+                    // the test adds at most zeros of the other sign at a bound
+                    // of +0 (-0 for T < 0), which widening never leaves (it
+                    // goes past the other zero then).  The
                     // row's extremes are NaN-propagating maxima and minima of
                     // the values, and the segments take the values' raw bits
                     // (the count pass turns them into keys).  Each lane counts
