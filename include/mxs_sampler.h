@@ -43,13 +43,15 @@ enum mxs_status {
     MXS_ERR_ALIGNMENT = 2,         /* logits not element-aligned or workspace not 256-byte aligned */
     MXS_ERR_WORKSPACE_TOO_SMALL = 3,
     MXS_ERR_VOCAB_TOO_LARGE = 4,   /* V > MXS_MAX_VOCAB */
-    MXS_ERR_HIP = 5                /* a HIP runtime call failed */
+    MXS_ERR_HIP = 5,               /* a HIP runtime call failed */
+    MXS_ERR_LDS_LIMIT = 6          /* the kernels' LDS limit could not be raised (hipFuncSetAttribute) */
 };
 
 /* Per-row outcome written to out_status (out_tokens holds -1 unless OK). */
 enum mxs_row_status {
     MXS_ROW_OK = 0,
-    MXS_ROW_BAD_HISTORY = 1,    /* a history id is outside [0, V) (torch: IndexError) */
+    MXS_ROW_BAD_HISTORY = 1,    /* a history id is outside [0, V) (torch: IndexError), or the
+                                   row's history range lies outside hist_ids */
     MXS_ROW_BAD_PARAM = 2,      /* temperature is NaN */
     MXS_ROW_NONFINITE = 3,      /* a tempered logit is NaN or the max is infinite (torch: multinomial error) */
     MXS_ROW_EMPTY_NUCLEUS = 4   /* top_p <= 0 removes every token (torch: multinomial error) */
@@ -86,7 +88,12 @@ size_t mxs_workspace_bytes(int B, int V);
  *   top_p         f32[B]  >= 1 or NaN => off (sampling.py:56)
  *   penalty       f32[B]  1 => off (sampling.py:38)
  *   hist_offsets  i32[B+1] CSR offsets into hist_ids, or NULL for no history
- *   hist_ids      i32[hist_offsets[B]] generated token ids (any order, repeats ok)
+ *   hist_ids      i32[n_hist_ids] generated token ids (any order, repeats ok)
+ *   n_hist_ids    number of ids in hist_ids (>= 0).  A row's history is read
+ *                 only when its penalty is not 1 (sampling.py:38); then
+ *                 offsets outside [0, n_hist_ids], or hist_offsets[r + 1] <
+ *                 hist_offsets[r], make the row MXS_ROW_BAD_HISTORY, and no id
+ *                 outside hist_ids is read.
  *   uniforms      f32[B]  one u in [0,1) per row (clamped into it), or NULL for u = 0
  *   out_tokens    i64[B]  sampled ids; -1 for rows whose status is not MXS_ROW_OK
  *   out_status    i32[B]  mxs_row_status per row, or NULL
@@ -97,7 +104,7 @@ size_t mxs_workspace_bytes(int B, int V);
 int mxs_sample(const void* logits, int dtype, int B, int V, int64_t ld,
                const float* temperature, const int32_t* top_k,
                const float* top_p, const float* penalty,
-               const int32_t* hist_offsets, const int32_t* hist_ids,
+               const int32_t* hist_offsets, const int32_t* hist_ids, int64_t n_hist_ids,
                const float* uniforms,
                int64_t* out_tokens, int32_t* out_status, float* out_probs,
                void* workspace, size_t workspace_bytes, mxs_stream_t stream);
@@ -111,14 +118,15 @@ int mxs_sample(const void* logits, int dtype, int B, int V, int64_t ld,
  * requests without repacking.  It replaces the per-step rebuild of each
  * request's history from req.output_ids (mini_engine/scheduler.py:43, 275-276,
  * consumed at mini_engine/sampling.py:38-45).  hist_begin and hist_end are
- * both i32[B] device arrays, or both NULL for no history; everything else is
- * as for mxs_sample.
+ * both i32[B] device arrays, or both NULL for no history; a non-empty range
+ * that leaves [0, n_hist_ids) makes its row MXS_ROW_BAD_HISTORY (when the
+ * row's penalty is not 1).  Everything else is as for mxs_sample.
  */
 int mxs_sample_ranges(const void* logits, int dtype, int B, int V, int64_t ld,
                       const float* temperature, const int32_t* top_k,
                       const float* top_p, const float* penalty,
                       const int32_t* hist_begin, const int32_t* hist_end, const int32_t* hist_ids,
-                      const float* uniforms,
+                      int64_t n_hist_ids, const float* uniforms,
                       int64_t* out_tokens, int32_t* out_status, float* out_probs,
                       void* workspace, size_t workspace_bytes, mxs_stream_t stream);
 

@@ -84,9 +84,10 @@ void sample(torch::Tensor logits, torch::Tensor temperature, torch::Tensor top_k
     // the offsets then select no ids.
     const int32_t* hids = nullptr;
     if (hist_ids) hids = hist_ids->numel() ? hist_ids->data_ptr<int32_t>() : hoff;
+    const int64_t nids = hist_ids ? hist_ids->numel() : 0;
     int st = mxs_sample(logits.data_ptr(), dtype, (int)B, (int)V, logits.stride(0),
                         temperature.data_ptr<float>(), top_k.data_ptr<int32_t>(),
-                        top_p.data_ptr<float>(), penalty.data_ptr<float>(), hoff, hids,
+                        top_p.data_ptr<float>(), penalty.data_ptr<float>(), hoff, hids, nids,
                         (const float*)opt_ptr(uniforms), out_tokens.data_ptr<int64_t>(),
                         out_status ? out_status->data_ptr<int32_t>() : nullptr,
                         out_probs ? out_probs->data_ptr<float>() : nullptr,
@@ -134,7 +135,7 @@ void sample_ranges(torch::Tensor logits, torch::Tensor temperature, torch::Tenso
                                temperature.data_ptr<float>(), top_k.data_ptr<int32_t>(),
                                top_p.data_ptr<float>(), penalty.data_ptr<float>(),
                                hist_begin.data_ptr<int32_t>(), hist_end.data_ptr<int32_t>(),
-                               hist_ids.data_ptr<int32_t>(),
+                               hist_ids.data_ptr<int32_t>(), hist_ids.numel(),
                                (const float*)opt_ptr(uniforms), out_tokens.data_ptr<int64_t>(),
                                out_status ? out_status->data_ptr<int32_t>() : nullptr,
                                out_probs ? out_probs->data_ptr<float>() : nullptr,

@@ -10,8 +10,10 @@ and `sample_requests_resident` / `sample_batch_ranges` read them there.
 
 from __future__ import annotations
 
+import math
 from typing import Optional, Sequence
 
+import numpy as np
 import torch
 
 from . import _native
@@ -79,6 +81,19 @@ class Sampler:
         return self.tokens
 
 
+def device_temperature(t: float) -> float:
+    """The float32 temperature a row is sampled with.  sampling.py:47 tests
+    the Python float (T == 0 is greedy) and :50 divides by it as a float32
+    scalar, so a non-zero T that is 0 in float32 (|T| < 2^-150) divides by
+    zero there, and torch.multinomial then rejects the row; such a row gets
+    NaN here, which the kernels report as a row error, instead of turning
+    greedy."""
+    t = float(t)
+    if t != 0.0 and np.float32(t) == 0.0:
+        return math.nan
+    return t
+
+
 def _normalize_history(ids: Sequence[int], V: int) -> list:
     """torch indexing rules of sampling.py:39-40: negative ids wrap once,
     anything else out of range raises IndexError."""
@@ -113,7 +128,7 @@ def pack_requests(params_list, histories, V: int, device, generators=None):
     f = buf.view(torch.float32)
     off = 0
     for r, (p, g) in enumerate(zip(params_list, gens)):
-        f[r] = float(p.temperature)
+        f[r] = device_temperature(p.temperature)
         buf[B + r] = int(p.top_k) if -2**31 <= int(p.top_k) < 2**31 else (2**31 - 1)
         f[2 * B + r] = float(p.top_p)
         f[3 * B + r] = float(p.repetition_penalty)
@@ -252,7 +267,7 @@ def pack_resident(params_list, store: HistoryStore, slots: Sequence[int], device
     buf = torch.empty(7 * B, dtype=torch.int32)
     f = buf.view(torch.float32)
     for r, (p, g) in enumerate(zip(params_list, gens)):
-        f[r] = float(p.temperature)
+        f[r] = device_temperature(p.temperature)
         buf[B + r] = int(p.top_k) if -2**31 <= int(p.top_k) < 2**31 else (2**31 - 1)
         f[2 * B + r] = float(p.top_p)
         f[3 * B + r] = float(p.repetition_penalty)

@@ -14,7 +14,17 @@ from __future__ import annotations
 
 import math
 
+import numpy as np
+
 from .sampling import SamplingParams
+
+
+def _f32(v):
+    """v as a float32 value (a Python float), or None if v is not a real number."""
+    if isinstance(v, bool) or not isinstance(v, (int, float)):
+        return None
+    with np.errstate(over="ignore"):
+        return float(np.float32(v))
 
 
 def params_from_request(body: dict) -> SamplingParams:
@@ -35,7 +45,7 @@ def params_from_request(body: dict) -> SamplingParams:
 def check_params(p: SamplingParams) -> None:
     """Raise ValueError naming every field out of range:
 
-    temperature         finite and >= 0 (NaN: MXS_ROW_BAD_PARAM; a negative
+    temperature         0, or finite and > 0 (NaN: MXS_ROW_BAD_PARAM; a negative
                         value reverses the order of the logits; inf makes
                         every row non-finite, MXS_ROW_NONFINITE)
     top_p               in (0, 1] (<= 0: MXS_ROW_EMPTY_NUCLEUS; NaN or > 1
@@ -46,19 +56,31 @@ def check_params(p: SamplingParams) -> None:
                         their signs)
     max_new_tokens      >= 1
     seed                an int or None
+
+    The sampler computes in float32, as the reference's tensor arithmetic
+    does (sampling.py:42-44, 50, 62 use the Python floats as float32
+    scalars), so the ranges are checked on the float32 values: a temperature
+    of 1e-50 is 0 in float32 (greedy, where the reference would divide by
+    zero), a top_p of 1e-50 is 0 (an empty nucleus), a penalty of 1e39 is
+    inf; all are rejected here.
     """
     bad = []
     t = p.temperature
-    if not (isinstance(t, (int, float)) and math.isfinite(t) and t >= 0.0):
-        bad.append(f"temperature must be a finite number >= 0, got {t!r}")
+    t32 = _f32(t)
+    if not (t32 is not None and math.isfinite(t32) and (t32 > 0.0 or t == 0.0)):
+        bad.append(f"temperature must be 0 or a number > 0 that stays finite and non-zero "
+                   f"in float32, got {t!r}")
     tp = p.top_p
-    if not (isinstance(tp, (int, float)) and 0.0 < tp <= 1.0):
-        bad.append(f"top_p must be in (0, 1], got {tp!r}")
+    tp32 = _f32(tp)
+    if not (tp32 is not None and 0.0 < tp32 and tp <= 1.0):
+        bad.append(f"top_p must be in (0, 1] and non-zero in float32, got {tp!r}")
     if not (isinstance(p.top_k, int) and p.top_k >= 0):
         bad.append(f"top_k must be an integer >= 0, got {p.top_k!r}")
     rp = p.repetition_penalty
-    if not (isinstance(rp, (int, float)) and math.isfinite(rp) and rp > 0.0):
-        bad.append(f"repetition_penalty must be a finite number > 0, got {rp!r}")
+    rp32 = _f32(rp)
+    if not (rp32 is not None and math.isfinite(rp32) and rp32 > 0.0):
+        bad.append(f"repetition_penalty must be a number > 0 that stays finite and non-zero "
+                   f"in float32, got {rp!r}")
     if not (isinstance(p.max_new_tokens, int) and p.max_new_tokens >= 1):
         bad.append(f"max_tokens must be an integer >= 1, got {p.max_new_tokens!r}")
     if p.seed is not None and not (isinstance(p.seed, int) and not isinstance(p.seed, bool)):

@@ -24,7 +24,7 @@ from dataclasses import dataclass, field
 import torch
 
 from . import _native
-from .batch import ROW_OK, _normalize_history, raise_row_status
+from .batch import ROW_OK, _normalize_history, device_temperature, raise_row_status
 
 
 @dataclass
@@ -77,7 +77,7 @@ def sample(
     H = len(hist)
     buf = torch.empty(8 + max(H, 1), dtype=torch.int32)
     f = buf.view(torch.float32)
-    f[0] = float(params.temperature)
+    f[0] = device_temperature(params.temperature)
     tk = int(params.top_k)
     buf[1] = tk if -2**31 <= tk < 2**31 else 2**31 - 1
     f[2] = float(params.top_p)

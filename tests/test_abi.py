@@ -15,7 +15,7 @@ ROOT = os.path.abspath(os.path.join(os.path.dirname(__file__), ".."))
 HEADER = os.path.join(ROOT, "include", "mxs_sampler.h")
 LIB = os.path.join(ROOT, "llm-inference-scheduler_amd", "mi355x_sampler", "_lib", "libmxs_sampler.so")
 
-OK, INVALID, ALIGN, SMALL_WS, VOCAB, HIP = range(6)
+OK, INVALID, ALIGN, SMALL_WS, VOCAB, HIP, LDS_LIMIT = range(7)
 MAX_VOCAB = 262144
 
 
@@ -45,10 +45,11 @@ def lib():
     p = ctypes.c_void_p
     L.mxs_sample.restype = ctypes.c_int
     L.mxs_sample.argtypes = [p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int64,
-                             p, p, p, p, p, p, p, p, p, p, p, ctypes.c_size_t, p]
+                             p, p, p, p, p, p, ctypes.c_int64, p, p, p, p, p, ctypes.c_size_t, p]
     L.mxs_sample_ranges.restype = ctypes.c_int
     L.mxs_sample_ranges.argtypes = [p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int64,
-                                    p, p, p, p, p, p, p, p, p, p, p, p, ctypes.c_size_t, p]
+                                    p, p, p, p, p, p, p, ctypes.c_int64, p, p, p, p, p,
+                                    ctypes.c_size_t, p]
     return L
 
 
@@ -68,6 +69,7 @@ def test_header_constants_match_the_python_layer():
     assert c["MXS_OK"] == OK and c["MXS_ERR_INVALID_ARGUMENT"] == INVALID
     assert c["MXS_ERR_ALIGNMENT"] == ALIGN and c["MXS_ERR_WORKSPACE_TOO_SMALL"] == SMALL_WS
     assert c["MXS_ERR_VOCAB_TOO_LARGE"] == VOCAB and c["MXS_ERR_HIP"] == HIP
+    assert c["MXS_ERR_LDS_LIMIT"] == LDS_LIMIT
     assert c["MXS_DTYPE_F32"] == 0 and c["MXS_DTYPE_F16"] == 1
     assert c["MXS_MAX_VOCAB"] == MAX_VOCAB == batch.MAX_VOCAB
     assert (c["MXS_ROW_OK"], c["MXS_ROW_BAD_HISTORY"], c["MXS_ROW_BAD_PARAM"],
@@ -79,8 +81,8 @@ def test_header_constants_match_the_python_layer():
 def test_version_and_status_strings(lib):
     assert lib.mxs_version().decode().startswith("mxs-sampler")
     assert "gfx950" in lib.mxs_version().decode()
-    texts = [lib.mxs_status_string(s).decode() for s in range(6)]
-    assert len(set(texts)) == 6 and all(texts)
+    texts = [lib.mxs_status_string(s).decode() for s in range(7)]
+    assert len(set(texts)) == 7 and all(texts)
     assert lib.mxs_status_string(99).decode()
 
 
@@ -101,12 +103,12 @@ P = ctypes.c_void_p
 
 
 def call(lib, logits=A, dtype=0, B=4, V=1000, ld=1000, temperature=A, top_k=A, top_p=A,
-         penalty=A, hist_offsets=None, hist_ids=None, uniforms=A, out_tokens=A,
+         penalty=A, hist_offsets=None, hist_ids=None, n_hist_ids=0, uniforms=A, out_tokens=A,
          out_status=A, out_probs=None, workspace=A, workspace_bytes=None):
     if workspace_bytes is None:
         workspace_bytes = 0 if B <= 0 or V <= 0 or V > MAX_VOCAB else lib.mxs_workspace_bytes(B, V)
     return lib.mxs_sample(P(logits), dtype, B, V, ld, P(temperature), P(top_k), P(top_p),
-                          P(penalty), P(hist_offsets), P(hist_ids), P(uniforms), P(out_tokens),
+                          P(penalty), P(hist_offsets), P(hist_ids), n_hist_ids, P(uniforms), P(out_tokens),
                           P(out_status), P(out_probs), P(workspace), workspace_bytes, None)
 
 
@@ -123,6 +125,7 @@ def test_sample_rejects_bad_arguments_before_launching(lib):
     assert call(lib, out_tokens=None) == INVALID
     assert call(lib, workspace=None) == INVALID
     assert call(lib, hist_offsets=A, hist_ids=None) == INVALID
+    assert call(lib, hist_offsets=A, hist_ids=A, n_hist_ids=-1) == INVALID
     assert call(lib, ld=999) == INVALID
     assert call(lib, logits=A + 2) == ALIGN                  # f32 rows need 4-byte alignment
     assert call(lib, workspace=A + 64) == ALIGN
@@ -130,10 +133,10 @@ def test_sample_rejects_bad_arguments_before_launching(lib):
 
 
 def call_ranges(lib, logits=A, dtype=0, B=4, V=1000, ld=1000, hist_begin=A, hist_end=A,
-                hist_ids=A, out_tokens=A, workspace=A):
+                hist_ids=A, n_hist_ids=16, out_tokens=A, workspace=A):
     ws = 0 if B <= 0 or V <= 0 or V > MAX_VOCAB else lib.mxs_workspace_bytes(B, V)
     return lib.mxs_sample_ranges(P(logits), dtype, B, V, ld, P(A), P(A), P(A), P(A),
-                                 P(hist_begin), P(hist_end), P(hist_ids), P(A), P(out_tokens),
+                                 P(hist_begin), P(hist_end), P(hist_ids), n_hist_ids, P(A), P(out_tokens),
                                  P(A), P(None), P(workspace), ws, None)
 
 
@@ -141,6 +144,7 @@ def test_sample_ranges_rejects_bad_arguments_before_launching(lib):
     assert call_ranges(lib, hist_begin=A, hist_end=None) == INVALID   # begin and end go together
     assert call_ranges(lib, hist_begin=None, hist_end=A) == INVALID
     assert call_ranges(lib, hist_ids=None) == INVALID                 # ranges need an id buffer
+    assert call_ranges(lib, n_hist_ids=-3) == INVALID
     assert call_ranges(lib, B=-1) == INVALID
     assert call_ranges(lib, V=MAX_VOCAB + 1, ld=MAX_VOCAB + 1) == VOCAB
     assert call_ranges(lib, logits=A + 2) == ALIGN

@@ -87,6 +87,18 @@ def test_parity_full_flat16(oracle, cuda):
     check(w, ref, tok, st, None)
 
 
+def test_parity_flat16_benchmark_batch(oracle, cuda):
+    """The flat16 benchmark shape itself, B = 1024 (one workgroup per row,
+    the instance without the small-batch hand-over), with the post-filter
+    probabilities of every row."""
+    w = make_workload("flat16")
+    assert w.B == 1024
+    say(f"[parity-full] flat16 B={w.B} V={w.V} with probabilities")
+    ref = run_oracle(oracle, w, probs=True)
+    tok, st, probs = run_gpu(w, cuda, probs=True)
+    check(w, ref, tok, st, probs)
+
+
 def _edge_rows(V, seed=7):
     rng = np.random.default_rng(seed)
     base = (2.0 * rng.standard_normal(V)).astype(np.float32)

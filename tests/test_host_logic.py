@@ -5,6 +5,7 @@ failure without a GPU.
 """
 
 import dataclasses
+import math
 import os
 import subprocess
 import sys
@@ -61,6 +62,18 @@ def test_pack_requests_layout_and_draws():
     u = d["uniforms"].tolist()
     assert u[1] == 0.0 and [u[0], u[2], u[3]] == ref
     assert gens[1].get_state().equal(torch.Generator().manual_seed(12).get_state())
+
+
+def test_temperatures_that_vanish_in_float32_become_row_errors():
+    # sampling.py:47 tests the Python float, :50 divides by a float32 zero
+    from mi355x_sampler.batch import device_temperature
+    assert device_temperature(0.0) == 0.0 and device_temperature(-0.0) == 0.0
+    assert math.isnan(device_temperature(1e-50)) and math.isnan(device_temperature(-1e-50))
+    assert device_temperature(1e-40) == 1e-40 and device_temperature(0.7) == 0.7
+    d = pack_requests([SamplingParams(temperature=1e-50), SamplingParams(temperature=0.0)],
+                      [[], []], 10, "cpu")
+    t = d["temperature"].tolist()
+    assert math.isnan(t[0]) and t[1] == 0.0
 
 
 def test_pack_requests_without_history():

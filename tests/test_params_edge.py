@@ -29,6 +29,10 @@ def test_defaults_and_keys_follow_the_worker():
     ("repetition_penalty", math.nan),
     ("max_tokens", 0),
     ("seed", "abc"), ("seed", 1.5),
+    # values that the float32 arithmetic of the chain turns into 0 or inf
+    ("temperature", 1e-50), ("temperature", 1e39),
+    ("top_p", 1e-50),
+    ("repetition_penalty", 1e-50), ("repetition_penalty", 1e39),
 ])
 def test_out_of_range_values_are_rejected(field, value):
     with pytest.raises(ValueError, match=field):
@@ -44,5 +48,6 @@ def test_every_bad_field_is_named():
 
 def test_edge_values_pass():
     for body in ({"temperature": 0.0}, {"top_p": 1.0}, {"top_p": 1e-6}, {"top_k": 0},
-                 {"top_k": 10**6}, {"repetition_penalty": 1e-3}, {"max_tokens": 1}, {"seed": 0}):
-        params_from_request(body)
+                 {"top_k": 10**6}, {"repetition_penalty": 1e-3}, {"max_tokens": 1}, {"seed": 0},
+                 {"temperature": 1e-40}, {"top_p": 1e-40}, {"repetition_penalty": 3e38}):
+        params_from_request(body)   # (1e-40 is a float32 subnormal, not 0)
