@@ -92,6 +92,49 @@ def time_cpu_baseline(w, budget_s: float, max_rows: int, threads: int = 0):
     }
 
 
+def margin_parity(w, ref, dev, max_rows: int) -> dict:
+    """The top-p cut against the reference's own chain (oracle/margins.py).
+    margin_rows counts the rows whose exact cut lies within margins.BAND of a
+    token's edge (where torch's fp32 prefix can keep a token more or less).
+    For up to max_rows rows (margin rows first) the GPU's post-filter
+    probabilities, from a launch over just those rows, are compared with
+    oracle/torch_chain.cpu_ref(stable=True) and with the fp64 chain."""
+    import numpy as np
+    import torch
+
+    from mi355x_sampler import sample_batch
+    from oracle import margins
+    stoch = np.nonzero((w.temperature != 0) & (w.top_p < 1.0) & (ref.status == 0))[0]
+    pm = ref.info["p_margin"]
+    order = stoch[np.argsort(pm[stoch], kind="stable")][:max_rows]
+    out = {"margin_band": margins.BAND, "margin_rows": int((pm[stoch] < margins.BAND).sum()),
+           "margin_sample_rows": [int(r) for r in order]}
+    if order.size == 0:
+        return out
+    sub = w.take(order)
+    probs = torch.zeros((sub.B, sub.V), dtype=torch.float32, device=dev)
+    tok, st = sample_batch(**sub.to_device(dev), out_probs=probs, return_status=True)
+    probs = probs.cpu().numpy()
+    cmp = {}
+    for i, r in enumerate(order):
+        cmp[int(r)] = margins.compare_row(sub.logits[i], margins.row_params(sub, i),
+                                          margins.row_history(sub, i), probs[i], pm[r],
+                                          ref.info["n_kept"][r])
+    s = margins.summarize(cmp, w.B)
+    out.update({
+        "sample_tokens_match": bool(np.array_equal(tok.cpu().numpy(), ref.tokens[order])),
+        "keep_diff_vs_torch_chain": {"rows": s["keep_diff_rows_vs_torch_chain"],
+                                     "max_tokens": s["max_keep_diff_vs_torch_chain"],
+                                     "max_prefix_distance_to_top_p":
+                                         s["max_prefix_window_of_diffs_vs_torch_chain"]},
+        "keep_diff_vs_fp64_chain_rows": s["keep_diff_rows_vs_fp64_chain"],
+        "max_dprob_vs_torch_chain": s["max_dprob_vs_torch_chain"],
+        "max_dprob_vs_torch_chain_off_boundary_tokens": s["max_dprob_off_cut_vs_torch_chain"],
+        "all_sample_rows_hold": s["all_rows_hold"],
+    })
+    return out
+
+
 def load_traffic(workload: str, B: int):
     """HBM bytes per call from the committed rocprofv3 counter summary
     (FETCH_SIZE and WRITE_SIZE, each scaled by a plain copy's reading)."""
@@ -140,6 +183,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
+    ap.add_argument("--margin-rows", type=int, default=16,
+                    help="rows (closest cuts first) whose GPU probabilities are compared with "
+                         "the reference's torch chain")
     ap.add_argument("--no-cold", action="store_true",
                     help="skip the timing with the MALL flushed before each call")
     ap.add_argument("--copy-bytes", type=int, default=0,
@@ -230,6 +276,7 @@ def main():
         st = s.status.cpu().numpy()
         parity = {"rows": int(w.B), "token_match": bool(np.array_equal(got, ref.tokens)),
                   "status_match": bool(np.array_equal(st, ref.status))}
+        parity.update(margin_parity(w, ref, dev, args.margin_rows))
 
     algo = w.algorithmic_bytes()
     mean_us = float(region_us)

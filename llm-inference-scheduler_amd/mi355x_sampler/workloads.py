@@ -68,6 +68,17 @@ class Workload:
         return (self.logits.nbytes + 4 * self.hist_ids.size + 16 * self.B
                 + 4 * stochastic + 8 * self.B)
 
+    def take(self, rows) -> "Workload":
+        """The given rows as a workload of their own (histories rebased)."""
+        rows = np.asarray(rows, dtype=np.int64)
+        hists = [self.hist_ids[self.hist_offsets[r]:self.hist_offsets[r + 1]] for r in rows]
+        off = np.zeros(rows.size + 1, np.int32)
+        off[1:] = np.cumsum([h.size for h in hists])
+        ids = np.concatenate(hists).astype(np.int32) if hists else np.zeros(0, np.int32)
+        return Workload(self.name, np.ascontiguousarray(self.logits[rows]), self.temperature[rows],
+                        self.top_k[rows], self.top_p[rows], self.penalty[rows], off, ids,
+                        self.uniforms[rows], dict(self.meta))
+
     def to_device(self, device):
         """Device tensors in sample_batch argument order."""
         import torch
