@@ -44,7 +44,8 @@ enum mxs_status {
     MXS_ERR_WORKSPACE_TOO_SMALL = 3,
     MXS_ERR_VOCAB_TOO_LARGE = 4,   /* V > MXS_MAX_VOCAB */
     MXS_ERR_HIP = 5,               /* a HIP runtime call failed */
-    MXS_ERR_LDS_LIMIT = 6          /* the kernels' LDS limit could not be raised (hipFuncSetAttribute) */
+    MXS_ERR_LDS_LIMIT = 6,         /* the kernels' LDS limit could not be raised (hipFuncSetAttribute) */
+    MXS_ERR_SCRATCH_LIMIT = 7      /* mxs_sample_noalloc: the batch needs more than its static scratch */
 };
 
 /* Per-row outcome written to out_status (out_tokens holds -1 unless OK). */
@@ -129,6 +130,32 @@ int mxs_sample_ranges(const void* logits, int dtype, int B, int V, int64_t ld,
                       int64_t n_hist_ids, const float* uniforms,
                       int64_t* out_tokens, int32_t* out_status, float* out_probs,
                       void* workspace, size_t workspace_bytes, mxs_stream_t stream);
+
+/*
+ * mxs_sample without a workspace argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops and harnesses
+ * that forbid allocation).  It has no counterpart in the reference, whose
+ * sampler (mini_engine/sampling.py:30-69) allocates freely through torch.
+ *
+ * It allocates nothing: the workspace is a static device array inside the
+ * library, MXS_NOALLOC_SCRATCH_BYTES bytes on each GPU, held from the
+ * library's load until the process ends; the first call on a device looks
+ * up that device's copy.  It serves every shape mxs_workspace_bytes() sizes
+ * at most MXS_NOALLOC_SCRATCH_BYTES (every valid shape of this version) and
+ * returns MXS_ERR_SCRATCH_LIMIT for any other.  The scratch of the current
+ * device (hipGetDevice) is used, so `stream` must belong to that device.
+ * All calls on one GPU share its scratch: calls that may overlap on one
+ * GPU (different streams, or different threads) race and must be
+ * serialized by the caller.  Arguments and results are as for mxs_sample.
+ */
+#define MXS_NOALLOC_SCRATCH_BYTES 3022848
+int mxs_sample_noalloc(const void* logits, int dtype, int B, int V, int64_t ld,
+                       const float* temperature, const int32_t* top_k,
+                       const float* top_p, const float* penalty,
+                       const int32_t* hist_offsets, const int32_t* hist_ids, int64_t n_hist_ids,
+                       const float* uniforms,
+                       int64_t* out_tokens, int32_t* out_status, float* out_probs,
+                       mxs_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -10,6 +10,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "mxs_sampler.h"
 #include "sampler_params.h"
 
@@ -21,6 +23,33 @@ namespace {
 // what k_slices hands over for batches of up to SPLIT_MAX_B rows (the same
 // size for every batch, so that a buffer sized once serves every batch).
 constexpr size_t WORKSPACE_BYTES = (SL_WS_BYTES + 255) & ~(size_t)255;
+
+// mxs_sample_noalloc's workspace: a file-scope device array, one copy per
+// GPU (each holds it from the library's load to the process's end).  Host
+// code never uses the array's name as an address: the first call on a
+// device asks the runtime for that device's copy (hipGetSymbolAddress) and
+// keeps the pointer, which is what the kernels receive.
+constexpr size_t SCRATCH_BYTES = MXS_NOALLOC_SCRATCH_BYTES;
+static_assert(WORKSPACE_BYTES <= SCRATCH_BYTES, "every valid shape fits the static scratch");
+constexpr int SCRATCH_MAX_DEVICES = 64;
+static __device__ __align__(256) unsigned char scratch[SCRATCH_BYTES];
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[SCRATCH_MAX_DEVICES];
+
+// The current device's copy of `scratch` (looked up once per device).
+int scratch_of_current_device(void** out)
+{
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= SCRATCH_MAX_DEVICES) return MXS_ERR_HIP;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return MXS_ERR_HIP;
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return MXS_OK;
+}
 
 }  // namespace
 
@@ -38,6 +67,7 @@ const char* mxs_status_string(int status)
     case MXS_ERR_VOCAB_TOO_LARGE: return "vocabulary larger than MXS_MAX_VOCAB";
     case MXS_ERR_HIP: return "HIP runtime error";
     case MXS_ERR_LDS_LIMIT: return "could not raise the kernels' LDS limit to the 152 KB they use (hipFuncSetAttribute failed)";
+    case MXS_ERR_SCRATCH_LIMIT: return "the batch needs more workspace than mxs_sample_noalloc's static scratch holds";
     default: return "unknown status";
     }
 }
@@ -138,6 +168,27 @@ int mxs_sample_ranges(const void* logits, int dtype, int B, int V, int64_t ld,
     return sample_impl(logits, dtype, B, V, ld, temperature, top_k, top_p, penalty, hist_begin, hist_end,
                        hist_ids, n_hist_ids, uniforms, out_tokens, out_status, out_probs, workspace,
                        workspace_bytes, stream);
+}
+
+int mxs_sample_noalloc(const void* logits, int dtype, int B, int V, int64_t ld,
+                       const float* temperature, const int32_t* top_k,
+                       const float* top_p, const float* penalty,
+                       const int32_t* hist_offsets, const int32_t* hist_ids, int64_t n_hist_ids,
+                       const float* uniforms,
+                       int64_t* out_tokens, int32_t* out_status, float* out_probs,
+                       mxs_stream_t stream)
+{
+    if (B == 0) return MXS_OK;
+    const size_t need = mxs_workspace_bytes(B, V);
+    if (need > SCRATCH_BYTES) return MXS_ERR_SCRATCH_LIMIT;
+    void* ws = nullptr;
+    if (need > 0) {   // (an invalid shape is rejected by sample_impl below)
+        const int st = scratch_of_current_device(&ws);
+        if (st != MXS_OK) return st;
+    }
+    return sample_impl(logits, dtype, B, V, ld, temperature, top_k, top_p, penalty, hist_offsets, nullptr,
+                       hist_ids, n_hist_ids, uniforms, out_tokens, out_status, out_probs,
+                       ws, ws ? SCRATCH_BYTES : 0, stream);
 }
 
 }  // extern "C"

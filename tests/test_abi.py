@@ -15,7 +15,7 @@ ROOT = os.path.abspath(os.path.join(os.path.dirname(__file__), ".."))
 HEADER = os.path.join(ROOT, "include", "mxs_sampler.h")
 LIB = os.path.join(ROOT, "llm-inference-scheduler_amd", "mi355x_sampler", "_lib", "libmxs_sampler.so")
 
-OK, INVALID, ALIGN, SMALL_WS, VOCAB, HIP, LDS_LIMIT = range(7)
+OK, INVALID, ALIGN, SMALL_WS, VOCAB, HIP, LDS_LIMIT, SCRATCH_LIMIT = range(8)
 MAX_VOCAB = 262144
 
 
@@ -54,8 +54,8 @@ def lib():
 
 
 def test_header_declares_the_expected_entry_points():
-    assert declared_functions() == ["mxs_sample", "mxs_sample_ranges", "mxs_status_string",
-                                    "mxs_version", "mxs_workspace_bytes"]
+    assert declared_functions() == ["mxs_sample", "mxs_sample_noalloc", "mxs_sample_ranges",
+                                    "mxs_status_string", "mxs_version", "mxs_workspace_bytes"]
 
 
 def test_every_declared_symbol_is_exported(lib):
@@ -69,7 +69,7 @@ def test_header_constants_match_the_python_layer():
     assert c["MXS_OK"] == OK and c["MXS_ERR_INVALID_ARGUMENT"] == INVALID
     assert c["MXS_ERR_ALIGNMENT"] == ALIGN and c["MXS_ERR_WORKSPACE_TOO_SMALL"] == SMALL_WS
     assert c["MXS_ERR_VOCAB_TOO_LARGE"] == VOCAB and c["MXS_ERR_HIP"] == HIP
-    assert c["MXS_ERR_LDS_LIMIT"] == LDS_LIMIT
+    assert c["MXS_ERR_LDS_LIMIT"] == LDS_LIMIT and c["MXS_ERR_SCRATCH_LIMIT"] == SCRATCH_LIMIT
     assert c["MXS_DTYPE_F32"] == 0 and c["MXS_DTYPE_F16"] == 1
     assert c["MXS_MAX_VOCAB"] == MAX_VOCAB == batch.MAX_VOCAB
     assert (c["MXS_ROW_OK"], c["MXS_ROW_BAD_HISTORY"], c["MXS_ROW_BAD_PARAM"],
@@ -81,9 +81,16 @@ def test_header_constants_match_the_python_layer():
 def test_version_and_status_strings(lib):
     assert lib.mxs_version().decode().startswith("mxs-sampler")
     assert "gfx950" in lib.mxs_version().decode()
-    texts = [lib.mxs_status_string(s).decode() for s in range(7)]
-    assert len(set(texts)) == 7 and all(texts)
+    texts = [lib.mxs_status_string(s).decode() for s in range(8)]
+    assert len(set(texts)) == 8 and all(texts)
     assert lib.mxs_status_string(99).decode()
+
+
+def test_noalloc_scratch_covers_every_valid_shape(lib):
+    scratch = header_constants()["MXS_NOALLOC_SCRATCH_BYTES"]
+    for B in (1, 2, 64, 65, 256, 1024, 4096):
+        for V in (1, 1000, 151936, MAX_VOCAB):
+            assert 0 < lib.mxs_workspace_bytes(B, V) <= scratch
 
 
 def test_workspace_bytes(lib):
