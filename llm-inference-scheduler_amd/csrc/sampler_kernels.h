@@ -2050,8 +2050,8 @@ __device__ __forceinline__ bool finish_counts(const Params& p, int r, RowStream<
 // thread's NS logits sx, the first at index se0): the lower edge of the
 // histogram bin holding the sample's j-th largest, j well above the expected
 // k * NSAMP / V; and theta = widen(est).  It only steers the stream; the
-// count pass checks it.  hist (2048) and s_cs (64) must be zero; called by
-// the whole workgroup.
+// count pass checks it.  hist (2048) must be zero; s_cs (64) receives the
+// sums of its groups of 32 bins; called by the whole workgroup.
 __device__ __forceinline__ void sample_bound(const float (&sx)[NSAMP / NT], int se0, uint32_t kk, int V, float T,
                                              bool neg, bool pen_inline, float pen, const uint32_t* bm,
                                              uint32_t* hist, uint32_t* s_cs, uint32_t& est, uint32_t& theta)
@@ -2077,13 +2077,26 @@ __device__ __forceinline__ void sample_bound(const float (&sx)[NSAMP / NT], int 
     const Reduced sr = block_reduce(smax, smin, 0u);   // (its barriers also order the zeroed hist)
     const uint32_t span = sr.max - sr.min;
     const int sh = span >= 2048u ? (32 - __builtin_clz(span)) - 11 : 0;
+    // Most of a sample crowds into a few bins at its low end, where lanes of
+    // one atomic instruction that hit the same counter serialize: each
+    // thread adds its equal bins at once, and the group sums are formed
+    // from the bins afterwards instead of by atomics of their own.
+    uint32_t b4[NS];
+#pragma unroll
+    for (int q = 0; q < NS; ++q) b4[q] = (sk4[q] - sr.min) >> sh;
 #pragma unroll
     for (int q = 0; q < NS; ++q) {
-        const uint32_t b = (sk4[q] - sr.min) >> sh;
-        atomicAdd(&hist[b], 1u);
-        atomicAdd(&s_cs[b >> 5], 1u);
+        bool first = true;
+        uint32_t c = 1;
+#pragma unroll
+        for (int q2 = 0; q2 < NS; ++q2) {
+            if (q2 < q) first = first && b4[q2] != b4[q];
+            if (q2 > q) c += b4[q2] == b4[q] ? 1u : 0u;
+        }
+        if (first) atomicAdd(&hist[b4[q]], c);
     }
     __syncthreads();
+    group_sums<uint32_t>(hist, s_cs);
     // (every wave finds the bin by itself)
     const WHit hb = wave_find_desc<uint32_t>(hist, (u64)s_cs[lane_id()], (u64)(js - 1u));
     est = sr.min + ((uint32_t)hb.bin << sh);
