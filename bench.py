@@ -178,7 +178,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="zipf",
-                    choices=["zipf", "greedy", "peaked", "single", "flat16"])
+                    choices=["zipf", "greedy", "peaked", "single", "flat16", "default", "zipf_k0"])
     ap.add_argument("--batch", type=int, default=None, help="override the workload's batch")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -305,6 +305,9 @@ def main():
                 "peaked": "B=64 x V=151936 fp32 N(0,1)+12 at 5 ids, T=0.7 k=50 p=0.9 pen=1.1, 512-id histories",
                 "single": "B=1 x V=151936 fp32 3*N(0,1), T=0.8 k=50 p=0.9 pen=1.1, 64-id history",
                 "flat16": "B=1024 x V=151936 fp16 N(0,1), T=0.7 k=0 p=0.95 pen=1.05, 2048-id histories",
+                "default": "B=256 x V=151936 fp32 Zipf rows, the reference's default parameters "
+                           "(T=0.7, top_k=0, top_p=1.0, penalty 1.0)",
+                "zipf_k0": "the zipf batch with top_k=0 on every 32nd row (8 rows)",
             }[args.workload] if args.batch is None else f"{args.workload} with B={w.B}",
             "B": int(w.B), "V": int(w.V),
         },

@@ -1089,7 +1089,10 @@ struct RowStream {
             }
         }
     }
-    template <bool PEN, bool ALL = false, class Elem, class TileEnd>
+    // VAL: tile_end(id, val) also gets val(i), the raw (unpenalized) value
+    // of slot i, read again from the tile's registers (they stay live until
+    // the next load into them).
+    template <bool PEN, bool ALL = false, bool VAL = false, class Elem, class TileEnd>
     __device__ __forceinline__ void run(const uint32_t* bm, float pen, Elem&& elem, TileEnd&& tile_end)
     {
         const int tid = threadIdx.x;
@@ -1097,26 +1100,37 @@ struct RowStream {
         auto vid = [&](int t) {
             return [=](int i) { return (t * TV + (i / VW) * NT + tid) * VW + i % VW; };
         };
+        auto end_of = [&](const vec_t (&b)[FU], int t) -> bool {
+            if constexpr (VAL) {
+                return tile_end(vid(t), [&](int i) {
+                    float xs[VW];
+                    IO::unpack(b[i / VW], xs);
+                    return xs[i % VW];
+                });
+            } else {
+                return tile_end(vid(t));
+            }
+        };
         // A holds tile t, Bf tile t + 1
         int t = 0;
         for (; t + 1 < nfull; t += 2) {
             proc<false, PEN, ALL>(A, t, bm, pen, elem);
-            if (tile_end(vid(t))) return;
+            if (end_of(A, t)) return;
             load(A, t + 2);
             proc<false, PEN, ALL>(Bf, t + 1, bm, pen, elem);
-            if (tile_end(vid(t + 1))) return;
+            if (end_of(Bf, t + 1)) return;
             load(Bf, t + 3);
         }
         if (t < nfull) {
             proc<false, PEN, ALL>(A, t, bm, pen, elem);
-            if (tile_end(vid(t))) return;
+            if (end_of(A, t)) return;
             ++t;
 #pragma unroll
             for (int j = 0; j < FU; ++j) A[j] = Bf[j];   // (one call site for the last tile)
         }
         if (t < ntile) {
             proc<true, PEN, ALL>(A, t, bm, pen, elem);
-            if (tile_end(vid(t))) return;
+            if (end_of(A, t)) return;
         }
         // the rest of the row (all of a row that is not 16-byte aligned), element by element
         for (int e0 = nvec * VW; e0 < V; e0 += FTILE) {
@@ -1139,7 +1153,11 @@ struct RowStream {
                     else elem(i, e, x);
                 }
             }
-            if (tile_end([=](int i) { return e0 + i * NT + tid; })) return;
+            if constexpr (VAL) {
+                if (tile_end([=](int i) { return e0 + i * NT + tid; }, [&](int i) { return xs[i]; })) return;
+            } else {
+                if (tile_end([=](int i) { return e0 + i * NT + tid; })) return;
+            }
         }
     }
     // run() with the inline penalty chosen at run time
@@ -1149,6 +1167,14 @@ struct RowStream {
     {
         if (pen_inline) run<true>(bm, pen, elem, tile_end);
         else run<false>(bm, pen, elem, tile_end);
+    }
+    // run_pen() whose tile_end gets each slot's raw value too: tile_end(id, val)
+    template <class Elem, class TileEnd>
+    __device__ __forceinline__ void run_pen_val(const uint32_t* bm, bool pen_inline, float pen, Elem&& elem,
+                                                TileEnd&& tile_end)
+    {
+        if (pen_inline) run<true, false, true>(bm, pen, elem, tile_end);
+        else run<false, false, true>(bm, pen, elem, tile_end);
     }
     // run_pen() visiting every slot: elem(i, e, x, valid)
     template <class Elem, class TileEnd>
@@ -1540,6 +1566,364 @@ __device__ __forceinline__ bool finish_wide(const Params& p, int r, float T, boo
             [&](auto&&) { return false; });
     }
     return true;
+}
+
+// ---------------------------------------------------------------- top-k off, two passes
+//
+// A row with top-k off takes part in the top-p cut and the draw as a whole
+// (sampling.py:56-69).  finish_wide2 reads it twice, with the penalty
+// applied from the history bitmap in both passes:
+//   pass 1   the row's extremes; every element at or above the sample's
+//            largest (penalized) value yhi into an exact list, the top list
+//            (per-wave segments, as the top-k stream fills them); every
+//            other element counted in one of 2048 bins linear in its value
+//            over the sample's range [ylo, yhi) (values below ylo in bin 0);
+//   between  the top list's exact masses (total W_top), and for every bin a
+//            lower and an upper bound on its mass, from its count and the
+//            masses of its value edges; so bounds on the total W, on the
+//            positions of the top-p cut and of the draw, and a window of
+//            bins for each that must hold it when it is not in the top list;
+//   pass 2   the exact mass of every element below yhi, summed in
+//            registers (no atomics), the mass of the elements above each
+//            window, and the elements of the two windows gathered.
+// The cut and the draw are then exact picks from the top list or from their
+// window (pick_in_set).  Values y are ordered like the tempered values:
+// y = x for T > 0, -x for T < 0, and l = y / |T|.
+//
+// The top list's threshold is widened over the rounding of y / |T|, so that
+// every element tied in l with it is in the list; a tie in l can still
+// straddle a bin boundary (bins are at least 1000 ulps wide, so a tie group
+// meets at most two bins), so each window is gathered with one more bin on
+// either side and the mass above it is counted above that wider range: the
+// positions inside the window proper are then exact.
+//
+// Returns 1 when the row is done (token, or a status); 0 when the general
+// path must take over after pass 1, with rd holding the penalized row's
+// extreme keys; -1 when the sample's range is degenerate (nothing read
+// beyond the sample; the caller streams the row as before).
+constexpr int TL_CAP = 2048;             // the top list (u64 keys where the mass histogram was)
+constexpr int W2_KC = KF_CK;             // pass 2: the cut's window (LCAP u64)
+constexpr int W2_KD = KF_CK + 8 * LCAP;  //         the draw's window (LCAP u64)
+constexpr int W2_SMH = KF_CK + 16 * LCAP;   // pick_in_set's masses (2048 u64)
+static_assert(W2_SMH + 16384 <= KF_HL, "the windows and pick_in_set's masses fit below the history list");
+static_assert(TL_CAP * 8 <= KF_H - KF_MH, "the top list fits where the mass histogram was");
+
+template <typename TIn>
+__device__ __forceinline__ int finish_wide2(const Params& p, int r, RowStream<TIn>& rs, float T, bool neg,
+                                            float top_p, float u, float pen, bool pen_on, const uint32_t* bm,
+                                            const float (&sx)[NSAMP / NT], int se0, unsigned char* smem,
+                                            uint32_t* CH, Reduced& rd, int64_t& tok, int32_t& st)
+{
+    constexpr int NS = NSAMP / NT;
+    __shared__ uint32_t w2_seg[NWAVES], w2_ovf, w2_cnt[2], w2_dummy;
+    __shared__ uint32_t w2_r[4][NWAVES];
+    __shared__ u64 w2_s[3][NWAVES];
+    const int tid = threadIdx.x, lane = lane_id(), wv = wave_id();
+    const int V = p.V;
+    const TIn* rowp = (const TIn*)p.logits + (size_t)r * (size_t)p.ld;
+    uint32_t* ck = (uint32_t*)(smem + KF_CK);
+    uint32_t* ci = (uint32_t*)(smem + KF_CI);
+    u64* TL = (u64*)(smem + KF_MH);
+    u64* KC = (u64*)(smem + W2_KC);
+    u64* KD = (u64*)(smem + W2_KD);
+    u64* SMH = (u64*)(smem + W2_SMH);
+    auto yv = [&](float x) { return neg ? -x : x; };
+    auto has_pen = [&](int e) { return pen_on && ((bm[e >> 5] >> (e & 31)) & 1u); };
+
+    // the sample's range of (penalized) values
+    uint32_t kmx = 0, kmn = 0xFFFFFFFFu;
+#pragma unroll
+    for (int q = 0; q < NS; ++q) {
+        float x = sx[q];
+        if (has_pen(se0 + q)) x = penalize(x, pen);
+        const uint32_t ky = okey(yv(x));
+        kmx = ky > kmx ? ky : kmx;
+        kmn = ky < kmn ? ky : kmn;
+    }
+    for (int b = tid; b < 2048; b += NT) CH[b] = 0;
+    if (tid == 0) { w2_ovf = 0; w2_cnt[0] = 0; w2_cnt[1] = 0; }
+    const Reduced sr = block_reduce(kmx, kmn, 0u);   // (its barriers also order the zeroed counts)
+    if (!(sr.max > SK_MIN && sr.max < 0xFF800000u && sr.min >= SK_MIN && sr.min < sr.max)) return -1;
+    const float yhi = okey_inv(widen_threshold(sr.max, T, neg)), ylo = okey_inv(sr.min);
+    const float dy = (yhi - ylo) * 0x1p-11f;
+    const float scale = 2048.0f / (yhi - ylo);
+    // (bins wider than 1000 ulps of the values at their edges, all finite)
+    const float umax = __builtin_fmaxf(__builtin_fabsf(yhi), __builtin_fabsf(ylo)) * 0x1p-23f;
+    if (!(yhi > ylo) || !__builtin_isfinite(scale) || !__builtin_isfinite(dy) || !(dy > 1000.0f * umax))
+        return -1;
+
+    // pass 1
+    const int w = wv;
+    uint32_t* wck = ck + w * FSEG;
+    uint32_t* wci = ci + w * FSEG;
+    uint32_t cw = 0;
+    constexpr uint32_t SEG_USE = FSEG - 64;
+    float fmx = -INFINITY, fmn = INFINITY;
+    float tx[FPT];
+    uint32_t nhit = 0;
+    auto bin_of = [&](float y) -> uint32_t {   // (a NaN goes to bin 0)
+        const float f = (y - ylo) * scale;
+        return f >= 1.0f ? (f < 2047.0f ? (uint32_t)f : 2047u) : 0u;
+    };
+    rs.run_pen_all(bm, pen_on, pen,
+        [&](int i, int, float x, bool valid) {
+            fmx = __builtin_elementwise_maximum(fmx, x);
+            fmn = __builtin_elementwise_minimum(fmn, x);
+            const float y = yv(x);
+            const bool top = valid && y >= yhi;
+            tx[i] = top ? x : __builtin_nanf("");
+            nhit += top ? 1u : 0u;
+            atomicAdd(valid && !top ? &CH[bin_of(y)] : &w2_dummy, 1u);   // (no branch per element)
+        },
+        [&](auto&& id) -> bool {
+            const uint32_t incl = wave_prefix_u32(nhit);
+            const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+            if (__builtin_expect(cw + tot > SEG_USE, 0)) {
+                if (lane == 0) __hip_atomic_store(&w2_ovf, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                cw = SEG_USE;   // (the rest of the row still counts toward the extremes)
+                nhit = 0;
+                return false;
+            }
+            uint32_t o = cw + incl - nhit;
+            const uint32_t dummy = SEG_USE + (uint32_t)lane;
+#pragma unroll
+            for (int i = 0; i < FPT; ++i) {
+                const bool h = tx[i] == tx[i];
+                const uint32_t a = h ? o : dummy;
+                wck[a] = f2u(tx[i]);
+                wci[a] = (uint32_t)id(i);
+                o += h ? 1u : 0u;
+            }
+            nhit = 0;
+            cw += tot;
+            return false;
+        });
+    uint32_t omax, omin;
+    if (fmx != fmx) {   // a NaN (both extremes carry it): keys that say so
+        omax = 0xFFFFFFFFu;
+        omin = 0u;
+    } else {
+        omax = neg ? selkey(fmn, true) : selkey(fmx, false);
+        omin = neg ? selkey(fmx, true) : selkey(fmn, false);
+    }
+    {
+        const uint32_t a0 = wave_max_u32(omax), a1 = wave_min_u32(omin);
+        if (lane == 0) { w2_r[0][w] = a0; w2_r[1][w] = a1; w2_seg[w] = cw; }
+    }
+    __syncthreads();
+    rd = Reduced{0u, 0xFFFFFFFFu, 0u};
+    uint32_t ntop = 0, off = 0;
+#pragma unroll
+    for (int v = 0; v < NWAVES; ++v) {
+        rd.max = w2_r[0][v] > rd.max ? w2_r[0][v] : rd.max;
+        rd.min = w2_r[1][v] < rd.min ? w2_r[1][v] : rd.min;
+        off += v < w ? w2_seg[v] : 0u;
+        ntop += w2_seg[v];
+    }
+    // NaN keys lie above the key of +inf and below that of -inf
+    const bool has_nan = rd.max > 0xFF800000u || rd.min < 0x007FFFFFu;
+    const bool has_inf = rd.max >= 0xFF800000u || rd.min <= 0x007FFFFFu;
+    if (has_nan || (has_inf && __builtin_isinf(T))) { st = MXS_ROW_NONFINITE; tok = -1; return 1; }
+    const float m = sel_inv(rd.max, neg) / T;
+    if (!isfinite(m)) { st = MXS_ROW_NONFINITE; tok = -1; return 1; }
+    if (top_p < 1.0f && !(top_p > 0.0f)) { st = MXS_ROW_EMPTY_NUCLEUS; tok = -1; return 1; }
+    if (w2_ovf || ntop > (uint32_t)TL_CAP) return 0;
+
+    // the top list's keys and exact masses
+    u64 part = 0;
+    for (uint32_t j = (uint32_t)lane; j < cw; j += 64) {
+        const float l = u2f(wck[j]) / T;
+        TL[off + j] = ((u64)vkey(l) << 32) | (u64)(0xFFFFFFFFu - wci[j]);
+        part += mass_of(l - m);
+    }
+    const u64 Wtop = block_sum<u64>(part);   // (its barriers publish TL and the counts)
+
+    // bounds on each bin's mass (this thread's bins 2047 - 4 tid - i, in
+    // descending order), padded for the polynomial's last-bit wiggles
+    const float aT = __builtin_fabsf(T);
+    auto mass_at = [&](float y) -> u64 { return mass_of(y / aT - m); };
+    u64 mlo[4], mhi[4], slo = 0, shi = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int b = 2047 - 4 * tid - i;
+        const u64 c = (u64)CH[b];
+        const float ye_lo = ylo + ((float)b - 0.01f) * dy;
+        float ye_hi = ylo + ((float)b + 1.01f) * dy;
+        ye_hi = b == 2047 || ye_hi > yhi ? yhi : ye_hi;
+        u64 lo = b == 0 ? 0ull : mass_at(ye_lo);
+        u64 hi = mass_at(ye_hi);
+        lo = lo > (lo >> 20) + 1 ? lo - (lo >> 20) - 1 : 0ull;
+        hi = hi + (hi >> 20) + 1;
+        mlo[i] = c * lo;
+        mhi[i] = c * hi;
+        slo += mlo[i];
+        shi += mhi[i];
+    }
+    u64 Blo, Bhi;
+    const u64 prelo0 = block_incl_scan<u64>(slo, &Blo) - slo;   // the mass bounds above this thread's bins
+    const u64 prehi0 = block_incl_scan<u64>(shi, &Bhi) - shi;
+    const u64 Wlo = Wtop + Blo, Whi = Wtop + Bhi;
+    // The bins that can hold a target position pos = q(W) + a (absolute;
+    // positions below Wtop are in the top list), q monotone with q(X) <= X,
+    // a in [a_lo, a_hi]: [lo, hi], or hi < lo for none.  For bin b with the
+    // mass Pre above it, M in it and Suf below it (all in the bulk),
+    // pos - (Wtop + Pre) = q(Wtop + Pre + M + Suf) - (Wtop + Pre) + a falls
+    // as Pre grows and rises with M + Suf; with independent bounds on the
+    // three this is bounded by evaluating q at Wtop + Blo + (Pre_hi - Pre_lo)
+    // and at Wtop + Bhi - (Pre_hi - Pre_lo).  (For q near 1, as for a draw
+    // deep in the tail, Pre's uncertainty hardly moves the position relative
+    // to the bin.)
+    auto window = [&](auto qx, long long a_lo, long long a_hi, int& lo, int& hi) {
+        int bmax = -1, bmin = 2048;
+        u64 pl = prelo0, ph = prehi0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int b = 2047 - 4 * tid - i;
+            const u64 dp = ph - pl;
+            const long long glo = (long long)qx(Wtop + Blo + dp) - (long long)(Wtop + ph) + a_lo;
+            const long long ghi = (long long)qx(Wtop + Bhi - dp) + 1 - (long long)(Wtop + pl) + a_hi;
+            if (mhi[i] > 0 && ghi >= 0 && glo < (long long)mhi[i]) {
+                bmax = b > bmax ? b : bmax;
+                bmin = b < bmin ? b : bmin;
+            }
+            pl += mlo[i];
+            ph += mhi[i];
+        }
+        const Reduced rw = block_reduce((uint32_t)(bmax + 1), (uint32_t)bmin, 0u);
+        hi = (int)rw.max - 1;
+        lo = (int)rw.min;
+    };
+    const bool bounded = top_p < 1.0f;
+    const float cu = clamp_uniform(u);
+    int c_lo = 2048, c_hi = -1, d_lo = 2048, d_hi = -1;
+    if (bounded) {
+        // the cut: t = ceil(p W) - 1 in [floor(p W) - 1, floor(p W)]
+        window([&](u64 X) { return floor_mul(top_p, X); }, -1, 0, c_lo, c_hi);
+        const u64 tlo = ceil_mul(top_p, Wlo) - 1, thi = ceil_mul(top_p, Whi) - 1;
+        if (thi >= Wtop) {
+            // the draw D = floor(u Wk), Wk = t + 1 + (part of the cut
+            // element's mass): at most wmax more than ceil(p W), wmax the
+            // largest mass an element of the cut's window (or of the top
+            // list, if the cut may lie there) can have
+            u64 wmax;
+            if (tlo < Wtop) {
+                wmax = 1ull << 45;
+            } else {
+                const int bt = c_hi + 1 < 2047 ? c_hi + 1 : 2047;
+                const float yt = bt == 2047 ? yhi : ylo + ((float)bt + 1.01f) * dy;
+                const u64 mt = mass_at(yt < yhi ? yt : yhi);
+                wmax = mt + (mt >> 20) + 1;
+            }
+            window([&](u64 X) { return floor_mul(cu, floor_mul(top_p, X)); }, -1, (long long)wmax + 2,
+                   d_lo, d_hi);
+        }
+    } else {
+        window([&](u64 X) { return floor_mul(cu, X); }, 0, 0, d_lo, d_hi);   // the draw D = floor(u W)
+    }
+    // The gathered ranges: one more bin on either side, as value thresholds
+    // [ya, yb) (an element is above a window iff y >= yb, in it iff
+    // ya <= y < yb; an empty window has ya = yb = yhi).  Pass 2 tests values
+    // only: a threshold may fall a rounding away from its bin's edge, which
+    // the spare bin on either side absorbs.
+    auto edge = [&](int b) -> float { return b <= 0 ? -INFINITY : (b >= 2048 ? yhi : ylo + (float)b * dy); };
+    const float yca = c_hi >= c_lo ? edge(c_lo - 1) : yhi, ycb = c_hi >= c_lo ? edge(c_hi + 2) : yhi;
+    const float yda = d_hi >= d_lo ? edge(d_lo - 1) : yhi, ydb = d_hi >= d_lo ? edge(d_hi + 2) : yhi;
+
+    // pass 2 (no branch per element: the rare window elements are marked,
+    // and written at the tile's end by the waves that have any)
+    rs.restart();
+    u64 wb = 0, ac = 0, ad = 0;
+    uint32_t mc = 0, md = 0;   // this tile's window elements, a bit per slot
+    rs.run_pen_val(bm, pen_on, pen,
+        [&](int i, int, float x) {
+            const float y = yv(x);
+            const float l = x / T;
+            const u64 wgt = y >= yhi ? 0ull : count_mass(1u, l - m);
+            wb += wgt;
+            ac += y >= ycb ? wgt : 0ull;
+            ad += y >= ydb ? wgt : 0ull;
+            mc |= (y >= yca && !(y >= ycb) ? 1u : 0u) << i;
+            md |= (y >= yda && !(y >= ydb) ? 1u : 0u) << i;
+        },
+        [&](auto&& id, auto&& val) -> bool {
+            if (__ballot((mc | md) != 0u)) {
+#pragma unroll
+                for (int i = 0; i < FPT; ++i) {
+                    if (((mc | md) >> i) & 1u) {
+                        const int e = id(i);
+                        float x = val(i);
+                        if (has_pen(e)) x = penalize(x, pen);
+                        const u64 key = ((u64)vkey(x / T) << 32) | (u64)(0xFFFFFFFFu - (uint32_t)e);
+                        if ((mc >> i) & 1u) {
+                            const uint32_t s = atomicAdd(&w2_cnt[0], 1u);
+                            if (s < (uint32_t)LCAP) KC[s] = key;
+                        }
+                        if ((md >> i) & 1u) {
+                            const uint32_t s = atomicAdd(&w2_cnt[1], 1u);
+                            if (s < (uint32_t)LCAP) KD[s] = key;
+                        }
+                    }
+                }
+            }
+            mc = 0;
+            md = 0;
+            return false;
+        });
+    {
+        const u64 a0 = wave_sum_u64(wb), a1 = wave_sum_u64(ac), a2 = wave_sum_u64(ad);
+        if (lane == 0) { w2_s[0][w] = a0; w2_s[1][w] = a1; w2_s[2][w] = a2; }
+    }
+    __syncthreads();
+    u64 WB = 0, AC = 0, AD = 0;
+#pragma unroll
+    for (int v = 0; v < NWAVES; ++v) { WB += w2_s[0][v]; AC += w2_s[1][v]; AD += w2_s[2][v]; }
+    const uint32_t nc = w2_cnt[0], nd = w2_cnt[1];
+    const u64 W = Wtop + WB;
+    if (W < Wlo || W > Whi || nc > (uint32_t)LCAP || nd > (uint32_t)LCAP) return 0;
+
+    // the cut and the draw (sampling.py:56-63, 69)
+    u64* SMHp = SMH;
+    uint32_t* SCH = CH;
+    u64 Wk = W, cutkey = 0;
+    if (bounded) {
+        const u64 t = ceil_mul(top_p, W) - 1;
+        SetPick c;
+        if (t < Wtop) {
+            c = pick_in_set(TL, (int)ntop, t, m, SMHp, SCH);
+            Wk = c.E + c.w;
+        } else {
+            const u64 x = t - Wtop;
+            if (x < AC || !(yca < ycb)) return 0;
+            c = pick_in_set(KC, (int)nc, x - AC, m, SMHp, SCH);
+            Wk = Wtop + AC + c.E + c.w;
+        }
+        if (!c.ok) return 0;
+        cutkey = c.key;
+    }
+    const u64 D = floor_mul(cu, Wk);
+    SetPick dp;
+    if (D < Wtop) {
+        dp = pick_in_set(TL, (int)ntop, D, m, SMHp, SCH);
+    } else {
+        const u64 x = D - Wtop;
+        if (x < AD || !(yda < ydb)) return 0;
+        dp = pick_in_set(KD, (int)nd, x - AD, m, SMHp, SCH);
+    }
+    if (!dp.ok) return 0;
+    tok = (int64_t)(0xFFFFFFFFu - (uint32_t)dp.key);
+    st = MXS_ROW_OK;
+    if (p.out_probs) {   // sampling.py:68 (a third read, only when the probabilities are asked for)
+        float* out = p.out_probs + (size_t)r * (size_t)V;
+        rs.restart();
+        rs.run_pen(bm, pen_on, pen,
+            [&](int, int e, float x) {
+                const float l = x / T;
+                const u64 key = ((u64)vkey(l) << 32) | (u64)(0xFFFFFFFFu - (uint32_t)e);
+                if (!bounded || key >= cutkey) out[e] = (float)((double)mass_of(l - m) / (double)Wk);
+            },
+            [&](auto&&) { return false; });
+    }
+    return 1;
 }
 
 // ---------------------------------------------------------------- fp16 rows, top-k off
@@ -2543,6 +2927,7 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
             Nfix = Nc;
         };
         uint32_t est = 0, cmax = 0;   // the sampled estimate; the buffer's largest penalized key
+        int wide2 = -1;               // finish_wide2: 1 done, 0 general path, -1 not taken
         bool segs = false;            // the candidates are in the stream's per-wave segments
         bool binned = false;          // ... and carry their bins, counts and final masses
         bool have_rd = false;         // rd holds the penalized row's extremes
@@ -2879,6 +3264,11 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                     });
                 if (!overflow) fix_up();
             }
+        } else if (mode == MODE_LARGE && (k <= 0 || k >= V) && V >= FAST_MIN_V &&
+                   (wide2 = finish_wide2<TIn>(p, r, rs, T, neg, top_p, u, pen, pen_on, bm, sx, se0, smem, hist,
+                                              rd, tok, st)) >= 0) {
+            // top-k off, two passes (done, or rd holds the extremes for the general path)
+            have_rd = true;
         } else {
             u64 best = 0;
             uint32_t kmin = 0;
@@ -2901,8 +3291,8 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
         // reversed keys of T < 0 swap the two ranges)
         const bool has_nan = rd.max > 0xFF800000u || rd.min < 0x007FFFFFu;
         const bool has_inf = rd.max >= 0xFF800000u || rd.min <= 0x007FFFFFu;
-        if (st != MXS_ROW_OK) {
-            // a history id outside [0, V), found after the stream
+        if (wide2 == 1 || st != MXS_ROW_OK) {
+            // finished by finish_wide2, or a history id outside [0, V) found after the stream
         } else if (__builtin_expect(has_nan || (has_inf && __builtin_isinf(T)), 0)) {
             st = MXS_ROW_NONFINITE;   // a NaN tempered logit heads the order (sampling.py:57-58)
         } else {
@@ -2977,7 +3367,7 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                                        (u64*)(smem + KF_MH), hist, tok, st);
                 }
             }
-            if (!done && mode == MODE_LARGE && (k <= 0 || k >= V)) {
+            if (!done && mode == MODE_LARGE && (k <= 0 || k >= V) && wide2 < 0) {
                 __syncthreads();
                 done = finish_wide<TIn>(p, r, T, neg, top_p, u, pen, pen_on, bm, hl, s_nh, rd.max, rd.min,
                                         (u64*)(smem + KF_MH),

@@ -20,6 +20,13 @@ Shapes (vocabulary V = 151,936, mini_engine/model/config.py:13):
             penalty ~ U[1.0, 1.3] over 1024 ids ~ U[0, V)
   "flat16"  B=1024, fp16 N(0,1); T=0.7, top_k=0, top_p=0.95, penalty=1.05
             over 2048 ids ~ U[0, V)
+  "default" B=256, fp32 Zipf-shaped rows as "zipf", with the reference's
+            default SamplingParams (mini_engine/sampling.py:16-19,
+            server/worker.py:56-59): T=0.7, top_k=0 (off), top_p=1.0 (off),
+            penalty 1.0, no history
+  "zipf_k0" the "zipf" batch (same seed, rows and parameters) with top_k = 0
+            (off) on every 32nd row, as the draw top_k ~ U{0..1000} gives
+            some batches
 """
 
 from __future__ import annotations
@@ -37,6 +44,8 @@ SHAPES = {
     "peaked": (1003, 64, np.float32, 512),
     "zipf": (1004, 256, np.float32, 1024),
     "flat16": (1005, 1024, np.float16, 2048),
+    "default": (1006, 256, np.float32, 0),
+    "zipf_k0": (1004, 256, np.float32, 1024),
 }
 
 
@@ -93,7 +102,7 @@ class Workload:
 
 def _row(name, seed, r, V, H):
     rng = np.random.default_rng([seed, r])
-    if name == "zipf":
+    if name in ("zipf", "zipf_k0"):
         T = rng.uniform(0.3, 1.5)
         k = int(rng.integers(0, 1001))
         p = rng.uniform(0.5, 1.0)
@@ -106,8 +115,12 @@ def _row(name, seed, r, V, H):
         T, k, p, pen = 0.7, 50, 0.9, 1.1
     elif name == "flat16":
         T, k, p, pen = 0.7, 0, 0.95, 1.05
+    elif name == "default":
+        T, k, p, pen = 0.7, 0, 1.0, 1.0
     else:
         raise KeyError(name)
+    if name == "zipf_k0" and r % 32 == 0:
+        k = 0
     u = rng.random(dtype=np.float32) if T != 0.0 else np.float32(0.0)
 
     if name == "peaked":
@@ -122,7 +135,7 @@ def _row(name, seed, r, V, H):
         hist = rng.integers(0, V, size=H)
         if name in ("single", "greedy"):
             x = (3.0 * rng.standard_normal(V)).astype(np.float32)
-        elif name == "zipf":
+        elif name in ("zipf", "zipf_k0", "default"):
             rank = rng.permutation(V) + 1
             x = (-1.1 * np.log(rank) + 0.1 * rng.standard_normal(V)).astype(np.float32)
         else:  # flat16

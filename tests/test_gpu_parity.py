@@ -61,7 +61,8 @@ def custom(name, logits, T, k, p, pen, hists, u):
 
 
 @pytest.mark.parametrize("name,B", [("single", 1), ("greedy", 16), ("peaked", 16),
-                                    ("zipf", 24), ("flat16", 3)])
+                                    ("zipf", 24), ("flat16", 3), ("default", 8), ("default", 96),
+                                    ("zipf_k0", 70)])
 def test_parity_small_batches(oracle, cuda, name, B):
     w = make_workload(name, B=B)
     say(f"[parity-small] {name} B={B} V={w.V}")
@@ -70,7 +71,7 @@ def test_parity_small_batches(oracle, cuda, name, B):
     check(w, ref, tok, st, probs)
 
 
-@pytest.mark.parametrize("name", ["greedy", "peaked", "zipf"])
+@pytest.mark.parametrize("name", ["greedy", "peaked", "zipf", "default", "zipf_k0"])
 def test_parity_full_batches(oracle, cuda, name):
     w = make_workload(name)
     say(f"[parity-full] {name} B={w.B} V={w.V}")
