@@ -172,6 +172,92 @@ def copy_calibration(dev, nbytes: int, steps: int, warmup: int):
           flush=True)
 
 
+FP32_MFMA_PEAK_TFLOPS = 157.3
+LM_HIDDEN = 896          # Qwen2.5-0.5B hidden size (mini_engine/model/config.py)
+
+
+def bench_lm_head(dev, steps: int, warmup: int, batches, parity: bool):
+    """The LM head of mini_engine/model/qwen2.py:176-183 (F.linear of the
+    last hidden states with the tied [151936, 896] embedding, fp32) on the
+    MFMA kernel, beside torch's F.linear, for each batch size, and the head
+    followed by the sampler (the Zipf batch's parameters on the head's
+    logits) with and without the head's row maxima.  One JSON line."""
+    import numpy as np
+    import torch
+    import torch.nn.functional as F
+
+    from mi355x_sampler import Sampler, lm_head
+    from mi355x_sampler.workloads import VOCAB, make_workload
+
+    stream = torch.cuda.current_stream(dev)
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(steps):
+            fn()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) * 1e3 / steps
+
+    g = torch.Generator(device=dev).manual_seed(0)
+    weight = 0.05 * torch.randn((VOCAB, LM_HIDDEN), generator=g, device=dev)
+    # what one pass over the weights costs by itself: torch's sum of them
+    read_us = timed(lambda: weight.sum())
+    rows = []
+    for B in batches:
+        log(f"[bench] lm_head B={B}")
+        hidden = torch.randn((B, LM_HIDDEN), generator=g, device=dev)
+        logits = torch.empty((B, VOCAB), device=dev)
+        best = torch.empty(B, dtype=torch.int64, device=dev)
+        us = timed(lambda: lm_head(hidden, weight, logits, best))
+        us_t = timed(lambda: F.linear(hidden, weight))
+        flops = 2.0 * B * LM_HIDDEN * VOCAB
+        nbytes = 4.0 * (VOCAB * LM_HIDDEN + B * LM_HIDDEN + B * VOCAB) + 8.0 * B
+        ent = {"B": B, "kernel_us": us, "tflops": flops / us * 1e-6,
+               "frac_of_fp32_mfma_peak": flops / us * 1e-6 / FP32_MFMA_PEAK_TFLOPS,
+               "hbm_gbps": nbytes / us * 1e-3, "frac_of_hbm_peak": nbytes / us * 1e-3 / HBM_PEAK_GBPS,
+               "torch_linear_us": us_t}
+        # the head and the sampler, against F.linear followed by the sampler,
+        # with the parameters of the greedy and the Zipf batches
+        s = Sampler(B, VOCAB, dev)
+        for params in ("greedy", "zipf"):
+            w = make_workload(params, B=B)
+            d = w.to_device(dev)
+            d.pop("logits")
+
+            def with_best():
+                lm_head(hidden, weight, logits, best)
+                s.ext.sample_head(logits, d["temperature"], d["top_k"], d["top_p"], d["penalty"],
+                                  d["hist_offsets"], d["hist_ids"], d["uniforms"],
+                                  s.tokens, s.status, None, best, s.workspace)
+
+            def plain():
+                s.run(F.linear(hidden, weight), **d)
+
+            e = {"head_and_sample_us": timed(with_best), "torch_linear_and_sample_us": timed(plain)}
+            if parity:
+                from oracle import oracle as orc
+                with_best()
+                torch.cuda.synchronize()
+                ref = orc.sample_rows(logits.cpu().numpy(), w.temperature, w.top_k, w.top_p, w.penalty,
+                                      w.hist_offsets, w.hist_ids, w.uniforms)
+                e["token_match"] = bool(np.array_equal(s.tokens.cpu().numpy(), ref.tokens))
+                e["status_match"] = bool(np.array_equal(s.status.cpu().numpy(), ref.status))
+            ent[params + "_params"] = e
+        rows.append(ent)
+    print(json.dumps({"metric": "LM head (fp32 MFMA) + sampler, [B, 896] x [151936, 896]^T",
+                      "unit": "us", "steps": steps, "warmup": warmup, "dtype": "fp32",
+                      "data": "synthetic (hidden N(0,1), weight N(0, 0.05^2); Zipf batch parameters)",
+                      "peak_fp32_mfma_tflops": FP32_MFMA_PEAK_TFLOPS,
+                      "weight_read_us": {"torch_sum": read_us,
+                                         "gbps": 4.0 * VOCAB * LM_HIDDEN / read_us * 1e-3},
+                      "rows": rows}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -191,6 +277,9 @@ def main():
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="instead of the sampler, time a plain device copy of this many bytes "
                          "(the reference point for HBM byte counters)")
+    ap.add_argument("--lm-head", default="",
+                    help="instead of the sampler, time the LM head (and head + sampler) for these "
+                         "comma-separated batch sizes")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -209,6 +298,10 @@ def main():
     torch.cuda.set_device(dev)
     if args.copy_bytes:
         copy_calibration(dev, args.copy_bytes, args.steps, args.warmup)
+        return
+    if args.lm_head:
+        bench_lm_head(dev, args.steps, args.warmup, [int(b) for b in args.lm_head.split(",")],
+                      not args.no_parity)
         return
     log(f"[bench] building workload {args.workload}")
     w = make_workload(args.workload, B=args.batch)

@@ -132,6 +132,42 @@ int mxs_sample_ranges(const void* logits, int dtype, int B, int V, int64_t ld,
                       void* workspace, size_t workspace_bytes, mxs_stream_t stream);
 
 /*
+ * The model's LM head, with the sampler's greedy statistic in its epilogue.
+ * Replaces F.linear(h[last_idx], self.lm_head) of
+ * mini_engine/model/qwen2.py:176-183 (the tied embedding of :92-96, fp32):
+ *
+ *   out_logits[r, v] = sum_k hidden[r, k] * weight[v, k]   (fp32; MFMA)
+ *   out_best[r]      = max over v of (key(out_logits[r, v]) << 32) | ~v
+ *
+ * with key the order-preserving key of the value (NaN above every value,
+ * -0 equal to +0), so the low word of out_best[r] is the bitwise complement
+ * of the row's first maximal index.  hidden is [B, ldh] and weight [V, ldw]
+ * (rows 16-byte aligned, ld a multiple of 4), out_logits [B, ldl] with
+ * ldl >= V, out_best [B] (8-byte aligned); all device memory.  The sums are
+ * fp32 in an order of the kernel's own, so a logit differs from another
+ * fp32 summation by rounding (at most D * 2^-23 * sum_k |hidden[r, k]
+ * weight[v, k]|).  Asynchronous on `stream`.
+ */
+int mxs_lm_head(const float* hidden, int B, int D, int64_t ldh, const float* weight, int V, int64_t ldw,
+                float* out_logits, int64_t ldl, uint64_t* out_best, mxs_stream_t stream);
+
+/*
+ * mxs_sample for logits that mxs_lm_head wrote, with its out_best as
+ * row_best (or NULL: then exactly mxs_sample).  A greedy row (temperature
+ * 0) without a penalty (penalty 1, or no history) takes its token from
+ * row_best and its logits are not read again; every other row is sampled
+ * from the logits as by mxs_sample.  row_best must come from the same
+ * logits.
+ */
+int mxs_sample_head(const void* logits, int dtype, int B, int V, int64_t ld,
+                    const float* temperature, const int32_t* top_k,
+                    const float* top_p, const float* penalty,
+                    const int32_t* hist_offsets, const int32_t* hist_ids, int64_t n_hist_ids,
+                    const float* uniforms,
+                    int64_t* out_tokens, int32_t* out_status, float* out_probs,
+                    const uint64_t* row_best, void* workspace, size_t workspace_bytes, mxs_stream_t stream);
+
+/*
  * mxs_sample without a workspace argument, for callers that cannot allocate
  * device memory (code under HIP graph capture, serving loops and harnesses
  * that forbid allocation).  It has no counterpart in the reference, whose

@@ -90,7 +90,7 @@ int sample_impl(const void* logits, int dtype, int B, int V, int64_t ld,
                 const int32_t* hbegin, const int32_t* hend, const int32_t* hist_ids,
                 int64_t n_hist_ids, const float* uniforms,
                 int64_t* out_tokens, int32_t* out_status, float* out_probs,
-                void* workspace, size_t workspace_bytes, mxs_stream_t stream)
+                const uint64_t* row_best, void* workspace, size_t workspace_bytes, mxs_stream_t stream)
 {
     if (B < 0 || V <= 0) return MXS_ERR_INVALID_ARGUMENT;
     if (V > MXS_MAX_VOCAB) return MXS_ERR_VOCAB_TOO_LARGE;
@@ -122,6 +122,7 @@ int sample_impl(const void* logits, int dtype, int B, int V, int64_t ld,
     p.out_status = out_status;
     p.out_probs = out_probs;
 
+    p.pre_best = (const unsigned long long*)row_best;
     p.sl_hdr = nullptr;
     p.sl_ent = nullptr;
     p.G = 0;
@@ -152,7 +153,7 @@ int mxs_sample(const void* logits, int dtype, int B, int V, int64_t ld,
                void* workspace, size_t workspace_bytes, mxs_stream_t stream)
 {
     return sample_impl(logits, dtype, B, V, ld, temperature, top_k, top_p, penalty, hist_offsets, nullptr,
-                       hist_ids, n_hist_ids, uniforms, out_tokens, out_status, out_probs, workspace,
+                       hist_ids, n_hist_ids, uniforms, out_tokens, out_status, out_probs, nullptr, workspace,
                        workspace_bytes, stream);
 }
 
@@ -166,7 +167,7 @@ int mxs_sample_ranges(const void* logits, int dtype, int B, int V, int64_t ld,
 {
     if ((hist_begin != nullptr) != (hist_end != nullptr)) return MXS_ERR_INVALID_ARGUMENT;
     return sample_impl(logits, dtype, B, V, ld, temperature, top_k, top_p, penalty, hist_begin, hist_end,
-                       hist_ids, n_hist_ids, uniforms, out_tokens, out_status, out_probs, workspace,
+                       hist_ids, n_hist_ids, uniforms, out_tokens, out_status, out_probs, nullptr, workspace,
                        workspace_bytes, stream);
 }
 
@@ -187,8 +188,36 @@ int mxs_sample_noalloc(const void* logits, int dtype, int B, int V, int64_t ld,
         if (st != MXS_OK) return st;
     }
     return sample_impl(logits, dtype, B, V, ld, temperature, top_k, top_p, penalty, hist_offsets, nullptr,
-                       hist_ids, n_hist_ids, uniforms, out_tokens, out_status, out_probs,
+                       hist_ids, n_hist_ids, uniforms, out_tokens, out_status, out_probs, nullptr,
                        ws, ws ? SCRATCH_BYTES : 0, stream);
+}
+
+int mxs_sample_head(const void* logits, int dtype, int B, int V, int64_t ld,
+                    const float* temperature, const int32_t* top_k,
+                    const float* top_p, const float* penalty,
+                    const int32_t* hist_offsets, const int32_t* hist_ids, int64_t n_hist_ids,
+                    const float* uniforms,
+                    int64_t* out_tokens, int32_t* out_status, float* out_probs,
+                    const uint64_t* row_best, void* workspace, size_t workspace_bytes, mxs_stream_t stream)
+{
+    return sample_impl(logits, dtype, B, V, ld, temperature, top_k, top_p, penalty, hist_offsets, nullptr,
+                       hist_ids, n_hist_ids, uniforms, out_tokens, out_status, out_probs, row_best, workspace,
+                       workspace_bytes, stream);
+}
+
+int mxs_lm_head(const float* hidden, int B, int D, int64_t ldh, const float* weight, int V, int64_t ldw,
+                float* out_logits, int64_t ldl, uint64_t* out_best, mxs_stream_t stream)
+{
+    if (B < 0 || D <= 0 || V <= 0) return MXS_ERR_INVALID_ARGUMENT;
+    if (B == 0) return MXS_OK;
+    if (!hidden || !weight || !out_logits || !out_best) return MXS_ERR_INVALID_ARGUMENT;
+    if (ldh < D || ldw < D || ldl < V) return MXS_ERR_INVALID_ARGUMENT;
+    if (((uintptr_t)hidden & 15u) || ((uintptr_t)weight & 15u) || (ldh & 3) || (ldw & 3) ||
+        ((uintptr_t)out_best & 7u) || ((uintptr_t)out_logits & 3u))
+        return MXS_ERR_ALIGNMENT;
+    const hipError_t e = launch_lm_head(hidden, B, D, (long long)ldh, weight, V, (long long)ldw, out_logits,
+                                        (long long)ldl, (unsigned long long*)out_best, (hipStream_t)stream);
+    return e == hipSuccess ? MXS_OK : MXS_ERR_HIP;
 }
 
 }  // extern "C"

@@ -2,8 +2,9 @@
 //
 // It checks tensor dtypes, shapes, devices and contiguity, takes torch's
 // current HIP stream for the logits' device and forwards raw pointers to
-// mxs_sample.  No compute happens here and nothing is allocated: the Python
-// layer (mi355x_sampler.batch) owns outputs and the workspace.
+// the C ABI (mxs_sample, mxs_sample_ranges, mxs_sample_head, mxs_lm_head).
+// No compute happens here and nothing is allocated: the Python layer
+// (mi355x_sampler.batch, mi355x_sampler.head) owns outputs and the workspace.
 #include <torch/extension.h>
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
@@ -44,12 +45,13 @@ int64_t workspace_bytes(int64_t B, int64_t V)
     return (int64_t)mxs_workspace_bytes((int)B, (int)V);
 }
 
-void sample(torch::Tensor logits, torch::Tensor temperature, torch::Tensor top_k,
-            torch::Tensor top_p, torch::Tensor penalty,
-            std::optional<torch::Tensor> hist_offsets, std::optional<torch::Tensor> hist_ids,
-            std::optional<torch::Tensor> uniforms, torch::Tensor out_tokens,
-            std::optional<torch::Tensor> out_status, std::optional<torch::Tensor> out_probs,
-            torch::Tensor workspace)
+// mxs_sample, or mxs_sample_head when row_best is given
+void sample_common(torch::Tensor logits, torch::Tensor temperature, torch::Tensor top_k,
+                   torch::Tensor top_p, torch::Tensor penalty,
+                   std::optional<torch::Tensor> hist_offsets, std::optional<torch::Tensor> hist_ids,
+                   std::optional<torch::Tensor> uniforms, torch::Tensor out_tokens,
+                   std::optional<torch::Tensor> out_status, std::optional<torch::Tensor> out_probs,
+                   const std::optional<torch::Tensor>& row_best, torch::Tensor workspace)
 {
     TORCH_CHECK(logits.is_cuda(), "logits must be on a GPU device");
     TORCH_CHECK(logits.dim() == 2, "logits must be [B, V]");
@@ -85,15 +87,77 @@ void sample(torch::Tensor logits, torch::Tensor temperature, torch::Tensor top_k
     const int32_t* hids = nullptr;
     if (hist_ids) hids = hist_ids->numel() ? hist_ids->data_ptr<int32_t>() : hoff;
     const int64_t nids = hist_ids ? hist_ids->numel() : 0;
-    int st = mxs_sample(logits.data_ptr(), dtype, (int)B, (int)V, logits.stride(0),
-                        temperature.data_ptr<float>(), top_k.data_ptr<int32_t>(),
-                        top_p.data_ptr<float>(), penalty.data_ptr<float>(), hoff, hids, nids,
-                        (const float*)opt_ptr(uniforms), out_tokens.data_ptr<int64_t>(),
-                        out_status ? out_status->data_ptr<int32_t>() : nullptr,
-                        out_probs ? out_probs->data_ptr<float>() : nullptr,
-                        workspace.data_ptr(), (size_t)workspace.numel(),
-                        (mxs_stream_t)stream.stream());
+    int st;
+    if (row_best) {
+        st = mxs_sample_head(logits.data_ptr(), dtype, (int)B, (int)V, logits.stride(0),
+                             temperature.data_ptr<float>(), top_k.data_ptr<int32_t>(),
+                             top_p.data_ptr<float>(), penalty.data_ptr<float>(), hoff, hids, nids,
+                             (const float*)opt_ptr(uniforms), out_tokens.data_ptr<int64_t>(),
+                             out_status ? out_status->data_ptr<int32_t>() : nullptr,
+                             out_probs ? out_probs->data_ptr<float>() : nullptr,
+                             (const uint64_t*)row_best->data_ptr(), workspace.data_ptr(),
+                             (size_t)workspace.numel(), (mxs_stream_t)stream.stream());
+        raise_status(st, "mxs_sample_head");
+        return;
+    }
+    st = mxs_sample(logits.data_ptr(), dtype, (int)B, (int)V, logits.stride(0),
+                    temperature.data_ptr<float>(), top_k.data_ptr<int32_t>(),
+                    top_p.data_ptr<float>(), penalty.data_ptr<float>(), hoff, hids, nids,
+                    (const float*)opt_ptr(uniforms), out_tokens.data_ptr<int64_t>(),
+                    out_status ? out_status->data_ptr<int32_t>() : nullptr,
+                    out_probs ? out_probs->data_ptr<float>() : nullptr,
+                    workspace.data_ptr(), (size_t)workspace.numel(),
+                    (mxs_stream_t)stream.stream());
     raise_status(st, "mxs_sample");
+}
+
+void sample(torch::Tensor logits, torch::Tensor temperature, torch::Tensor top_k,
+            torch::Tensor top_p, torch::Tensor penalty,
+            std::optional<torch::Tensor> hist_offsets, std::optional<torch::Tensor> hist_ids,
+            std::optional<torch::Tensor> uniforms, torch::Tensor out_tokens,
+            std::optional<torch::Tensor> out_status, std::optional<torch::Tensor> out_probs,
+            torch::Tensor workspace)
+{
+    sample_common(logits, temperature, top_k, top_p, penalty, hist_offsets, hist_ids, uniforms, out_tokens,
+                  out_status, out_probs, std::nullopt, workspace);
+}
+
+// mxs_sample_head: greedy rows without a penalty take their token from
+// row_best, the maxima lm_head wrote for these logits
+void sample_head(torch::Tensor logits, torch::Tensor temperature, torch::Tensor top_k,
+                 torch::Tensor top_p, torch::Tensor penalty,
+                 std::optional<torch::Tensor> hist_offsets, std::optional<torch::Tensor> hist_ids,
+                 std::optional<torch::Tensor> uniforms, torch::Tensor out_tokens,
+                 std::optional<torch::Tensor> out_status, std::optional<torch::Tensor> out_probs,
+                 torch::Tensor row_best, torch::Tensor workspace)
+{
+    check_dev(row_best, logits, "row_best", torch::kInt64, logits.dim() == 2 ? logits.size(0) : -1);
+    sample_common(logits, temperature, top_k, top_p, penalty, hist_offsets, hist_ids, uniforms, out_tokens,
+                  out_status, out_probs, row_best, workspace);
+}
+
+// logits = hidden . weight^T and the rows' packed maxima (mxs_lm_head)
+void lm_head(torch::Tensor hidden, torch::Tensor weight, torch::Tensor out_logits, torch::Tensor out_best)
+{
+    TORCH_CHECK(hidden.is_cuda(), "hidden must be on a GPU device");
+    TORCH_CHECK(hidden.dim() == 2 && weight.dim() == 2 && out_logits.dim() == 2,
+                "hidden [B, D], weight [V, D] and out_logits [B, V] are matrices");
+    const int64_t B = hidden.size(0), D = hidden.size(1), V = weight.size(0);
+    TORCH_CHECK(weight.size(1) == D, "weight must be [V, ", D, "], got ", weight.sizes());
+    TORCH_CHECK(out_logits.size(0) == B && out_logits.size(1) == V, "out_logits must be [", B, ", ", V, "]");
+    for (const auto* t : {&hidden, &weight, &out_logits}) {
+        TORCH_CHECK(t->device() == hidden.device(), "all tensors must be on ", hidden.device());
+        TORCH_CHECK(t->scalar_type() == torch::kFloat32, "hidden, weight and out_logits must be float32");
+        TORCH_CHECK(t->stride(1) == 1, "rows must be contiguous");
+    }
+    check_dev(out_best, hidden, "out_best", torch::kInt64, B);
+    TORCH_CHECK(B <= INT32_MAX && D <= INT32_MAX && V <= INT32_MAX, "sizes must fit in int32");
+    const c10::DeviceGuard guard(hidden.device());
+    auto stream = c10::hip::getCurrentHIPStream();
+    int st = mxs_lm_head(hidden.data_ptr<float>(), (int)B, (int)D, hidden.stride(0), weight.data_ptr<float>(),
+                         (int)V, weight.stride(0), out_logits.data_ptr<float>(), out_logits.stride(0),
+                         (uint64_t*)out_best.data_ptr(), (mxs_stream_t)stream.stream());
+    raise_status(st, "mxs_lm_head");
 }
 
 // The same launch with row r's history at hist_ids[hist_begin[r], hist_end[r])
@@ -155,6 +219,14 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m)
           py::arg("logits"), py::arg("temperature"), py::arg("top_k"), py::arg("top_p"),
           py::arg("penalty"), py::arg("hist_offsets"), py::arg("hist_ids"), py::arg("uniforms"),
           py::arg("out_tokens"), py::arg("out_status"), py::arg("out_probs"), py::arg("workspace"));
+    m.def("sample_head", &sample_head,
+          "sample with the LM head's row maxima (see mxs_sample_head)",
+          py::arg("logits"), py::arg("temperature"), py::arg("top_k"), py::arg("top_p"),
+          py::arg("penalty"), py::arg("hist_offsets"), py::arg("hist_ids"), py::arg("uniforms"),
+          py::arg("out_tokens"), py::arg("out_status"), py::arg("out_probs"), py::arg("row_best"),
+          py::arg("workspace"));
+    m.def("lm_head", &lm_head, "logits = hidden . weight^T with the rows' packed maxima (mxs_lm_head)",
+          py::arg("hidden"), py::arg("weight"), py::arg("out_logits"), py::arg("out_best"));
     m.def("sample_ranges", &sample_ranges,
           "sample one token per row, histories as [begin, end) ranges of a device id buffer",
           py::arg("logits"), py::arg("temperature"), py::arg("top_k"), py::arg("top_p"),

@@ -1620,7 +1620,6 @@ __device__ __forceinline__ int finish_wide2(const Params& p, int r, RowStream<TI
     __shared__ u64 w2_s[3][NWAVES];
     const int tid = threadIdx.x, lane = lane_id(), wv = wave_id();
     const int V = p.V;
-    const TIn* rowp = (const TIn*)p.logits + (size_t)r * (size_t)p.ld;
     uint32_t* ck = (uint32_t*)(smem + KF_CK);
     uint32_t* ci = (uint32_t*)(smem + KF_CI);
     u64* TL = (u64*)(smem + KF_MH);
@@ -2526,7 +2525,8 @@ __global__ __launch_bounds__(NT, 1) void k_slices(Params p, uint32_t* hdr_all, u
     const bool pen_on = (pen != 1.0f) && (h1 > h0);
     const bool defer = pen_on && !neg && pen >= 1.0f && pen <= 3.402823466e38f;
     const bool topk = mode == MODE_TOPK && V >= FAST_MIN_V && (!pen_on || defer);
-    const bool greedy = mode == MODE_GREEDY && !pen_on;
+    // (a greedy row with the LM head's maximum needs no slices)
+    const bool greedy = mode == MODE_GREEDY && !pen_on && !p.pre_best;
     if ((!topk && !greedy) || hbad) {
         if (tid == 0) hdr[0] = SL_NONE;
         return;
@@ -2684,7 +2684,9 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
     const int se0 = (((tid >> 3) * (V >> 6)) & ~31) + (tid & 7) * NS;   // this thread's first sample
 #pragma unroll
     for (int q = 0; q < NS; ++q) sx[q] = VecIO<TIn>::one(rowp, se0 + q < V ? se0 + q : V - 1);
-    RowStream<TIn> rs(rowp, V, !SPLIT);   // (after k_slices: only for rows it did not take)
+    // (after k_slices, or with the LM head's maxima: issued later, for the rows that stream)
+    const bool early = !SPLIT && !p.pre_best;
+    RowStream<TIn> rs(rowp, V, early);
     __builtin_amdgcn_sched_barrier(0);   // (the loads above stay ahead of the reads below)
     const float T = __builtin_bit_cast(float, (uint32_t)__builtin_amdgcn_readlane((int)pv, 0));
     const int k = __builtin_amdgcn_readlane((int)pv, 1);
@@ -2700,12 +2702,12 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
     RowMode mode = classify(T, k, V);
     // every slice of the row handed over its part: the candidates replace the stream
     bool split = false;
-    if constexpr (SPLIT) {
-        split = !__ballot(lane < p.G && sln == SL_NONE);
-        if (!split) rs.restart();
-    }
+    if constexpr (SPLIT) split = !__ballot(lane < p.G && sln == SL_NONE);
     const bool neg = T < 0.0f;
     const bool pen_on = (pen != 1.0f) && (h1 > h0);
+    // a greedy row without a penalty takes the LM head's maximum (sampling.py:47-48)
+    const bool head_best = p.pre_best && mode == MODE_GREEDY && !pen_on && !hbad;
+    if (!early && !split && !head_best) rs.restart();
     int64_t tok = -1;
     int32_t st = hbad ? MXS_ROW_BAD_HISTORY : MXS_ROW_OK;
 
@@ -2881,9 +2883,9 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
 
     if (st == MXS_ROW_OK && mode == MODE_GREEDY) {   // sampling.py:47-48
         auto gkey = [](float x) -> uint32_t { return (x != x) ? 0xFFFFFFFFu : vkey(x); };   // NaN is the maximum
-        u64 best = 0;
+        u64 best = head_best ? p.pre_best[r] : 0ull;
         uint32_t kmin;
-        bool have = split || (raw_ok && raw_extremes(gkey, best, kmin));
+        bool have = head_best || split || (raw_ok && raw_extremes(gkey, best, kmin));
         if (split) {   // the slices' maxima
             const uint32_t* h = p.sl_hdr + (size_t)(r * p.G + (lane < p.G ? lane : 0)) * SL_HDR;
             const u64 sb = lane < p.G ? (((u64)h[6] << 32) | h[5]) : 0ull;

@@ -33,6 +33,9 @@ struct Params {
     const uint32_t* sl_hdr;
     const uint32_t* sl_ent;
     int G;
+    // the rows' packed maxima from the LM head's epilogue (NULL: none):
+    // (greedy key << 32) | ~index, the token of a greedy row without a penalty
+    const unsigned long long* pre_best;
 };
 
 // ---------------------------------------------------------------- small batches
@@ -61,5 +64,9 @@ template <typename TIn>
 hipError_t launch_fused(const Params& p, hipStream_t s, bool& lds_error);
 template <typename TIn>
 hipError_t launch_split(const Params& p, hipStream_t s, bool& lds_error);
+
+// k_lmhead.hip: logits = hidden . weight^T and the rows' packed maxima
+hipError_t launch_lm_head(const float* H, int B, int D, long long ldh, const float* W, int V, long long ldw,
+                          float* C, long long ldc, unsigned long long* best, hipStream_t s);
 
 }  // namespace mxs

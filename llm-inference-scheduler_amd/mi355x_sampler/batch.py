@@ -32,7 +32,8 @@ def sample_batch(logits: torch.Tensor, temperature: torch.Tensor, top_k: torch.T
                  hist_ids: Optional[torch.Tensor] = None,
                  uniforms: Optional[torch.Tensor] = None,
                  out_probs: Optional[torch.Tensor] = None,
-                 return_status: bool = False):
+                 return_status: bool = False,
+                 row_best: Optional[torch.Tensor] = None):
     """Sample one token per row of `logits` ([B, V], float32 or float16).
 
     temperature f32[B] (0 = greedy), top_k i32[B] (<= 0 off), top_p f32[B]
@@ -41,6 +42,8 @@ def sample_batch(logits: torch.Tensor, temperature: torch.Tensor, top_k: torch.T
     the logits' device.  Returns int64[B] token ids on the device (-1 for rows
     whose status is not ok), plus int32[B] row statuses if return_status.
     out_probs, if given, is filled with the post-filter probabilities [B, V].
+    row_best, if given, holds the row maxima that `head.lm_head` wrote with
+    these logits: greedy rows without a penalty take their token from it.
     The launch is asynchronous on the current stream.
     """
     _native.require_gpu(logits.device)
@@ -50,8 +53,12 @@ def sample_batch(logits: torch.Tensor, temperature: torch.Tensor, top_k: torch.T
     tokens = torch.empty(B, dtype=torch.int64, device=dev)
     status = torch.empty(B, dtype=torch.int32, device=dev)
     ws = _native.workspace(dev, B, V)
-    ext.sample(logits, temperature, top_k, top_p, penalty, hist_offsets, hist_ids, uniforms,
-               tokens, status, out_probs, ws)
+    if row_best is None:
+        ext.sample(logits, temperature, top_k, top_p, penalty, hist_offsets, hist_ids, uniforms,
+                   tokens, status, out_probs, ws)
+    else:
+        ext.sample_head(logits, temperature, top_k, top_p, penalty, hist_offsets, hist_ids, uniforms,
+                        tokens, status, out_probs, row_best, ws)
     return (tokens, status) if return_status else tokens
 
 

@@ -50,12 +50,19 @@ def lib():
     L.mxs_sample_ranges.argtypes = [p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int64,
                                     p, p, p, p, p, p, p, ctypes.c_int64, p, p, p, p, p,
                                     ctypes.c_size_t, p]
+    L.mxs_sample_head.restype = ctypes.c_int
+    L.mxs_sample_head.argtypes = [p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int64,
+                                  p, p, p, p, p, p, ctypes.c_int64, p, p, p, p, p, p, ctypes.c_size_t, p]
+    L.mxs_lm_head.restype = ctypes.c_int
+    L.mxs_lm_head.argtypes = [p, ctypes.c_int, ctypes.c_int, ctypes.c_int64, p, ctypes.c_int, ctypes.c_int64,
+                              p, ctypes.c_int64, p, p]
     return L
 
 
 def test_header_declares_the_expected_entry_points():
-    assert declared_functions() == ["mxs_sample", "mxs_sample_noalloc", "mxs_sample_ranges",
-                                    "mxs_status_string", "mxs_version", "mxs_workspace_bytes"]
+    assert declared_functions() == ["mxs_lm_head", "mxs_sample", "mxs_sample_head", "mxs_sample_noalloc",
+                                    "mxs_sample_ranges", "mxs_status_string", "mxs_version",
+                                    "mxs_workspace_bytes"]
 
 
 def test_every_declared_symbol_is_exported(lib):
@@ -157,6 +164,46 @@ def test_sample_ranges_rejects_bad_arguments_before_launching(lib):
     assert call_ranges(lib, logits=A + 2) == ALIGN
     assert call_ranges(lib, out_tokens=None) == INVALID
     assert call_ranges(lib, B=0, logits=None, out_tokens=None, workspace=None) == OK
+
+
+def call_head(lib, hidden=A, B=4, D=896, ldh=896, weight=A, V=1000, ldw=896, logits=A, ldl=1000, best=A):
+    return lib.mxs_lm_head(P(hidden), B, D, ldh, P(weight), V, ldw, P(logits), ldl, P(best), None)
+
+
+def test_lm_head_rejects_bad_arguments_before_launching(lib):
+    assert call_head(lib, B=-1) == INVALID
+    assert call_head(lib, D=0) == INVALID
+    assert call_head(lib, V=0) == INVALID
+    assert call_head(lib, hidden=None) == INVALID
+    assert call_head(lib, weight=None) == INVALID
+    assert call_head(lib, logits=None) == INVALID
+    assert call_head(lib, best=None) == INVALID
+    assert call_head(lib, ldh=895) == INVALID         # strides cover a row
+    assert call_head(lib, ldw=100) == INVALID
+    assert call_head(lib, ldl=999) == INVALID
+    assert call_head(lib, hidden=A + 4) == ALIGN        # rows are read as 16-byte vectors
+    assert call_head(lib, weight=A + 8) == ALIGN
+    assert call_head(lib, D=897, ldh=897, ldw=900) == ALIGN
+    assert call_head(lib, D=897, ldh=900, ldw=898) == ALIGN
+    assert call_head(lib, best=A + 4) == ALIGN
+    assert call_head(lib, logits=A + 2) == ALIGN
+    assert call_head(lib, B=0, hidden=None, weight=None, logits=None, best=None) == OK
+
+
+def test_sample_head_checks_as_sample_does(lib):
+    def ch(**kw):
+        a = dict(logits=A, B=4, V=1000, ld=1000, out_tokens=A, workspace=A)
+        a.update(kw)
+        ws = lib.mxs_workspace_bytes(4, 1000)
+        return lib.mxs_sample_head(P(a["logits"]), 0, a["B"], a["V"], a["ld"], P(A), P(A), P(A), P(A),
+                                   P(None), P(None), 0, P(A), P(a["out_tokens"]), P(A), P(None), P(A),
+                                   P(a["workspace"]), ws, None)
+    assert ch(B=-1) == INVALID
+    assert ch(ld=999) == INVALID
+    assert ch(logits=A + 2) == ALIGN
+    assert ch(out_tokens=None) == INVALID
+    assert ch(workspace=None) == INVALID
+    assert ch(B=0, logits=None, out_tokens=None, workspace=None) == OK
 
 
 def test_empty_batch_is_a_no_op(lib):
