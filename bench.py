@@ -371,6 +371,28 @@ def main():
                   "status_match": bool(np.array_equal(st, ref.status))}
         parity.update(margin_parity(w, ref, dev, args.margin_rows))
 
+    dropin = None
+    if w.B == 1:
+        # the drop-in sample() of the single-row callers (mini_engine/generate.py:71,
+        # scheduler.py:275): per call, wall clock, host work and the one sync included
+        from mi355x_sampler import SamplingParams, sample as dropin_sample
+        prm = SamplingParams(temperature=float(w.temperature[0]), top_k=int(w.top_k[0]),
+                             top_p=float(w.top_p[0]), repetition_penalty=float(w.penalty[0]))
+        hist = w.hist_ids[w.hist_offsets[0]:w.hist_offsets[1]].tolist()
+        row = d["logits"][0]
+        row_host = torch.from_numpy(w.logits[0].copy())
+        gen = torch.Generator().manual_seed(0)
+        dropin = {}
+        for key, x in (("device_logits_us", row), ("host_logits_us", row_host)):
+            for _ in range(args.warmup):
+                dropin_sample(x, prm, hist, gen)
+            torch.cuda.synchronize()
+            n = max(args.steps, 50)
+            t1 = time.perf_counter()
+            for _ in range(n):
+                dropin_sample(x, prm, hist, gen)
+            dropin[key] = 1e6 * (time.perf_counter() - t1) / n
+
     algo = w.algorithmic_bytes()
     mean_us = float(region_us)
     achieved = algo / (mean_us * 1e-6) / 1e9
@@ -417,6 +439,8 @@ def main():
         "cold_mall": cold,
         "parity_vs_oracle": parity,
     }
+    if dropin is not None:
+        out["dropin_sample"] = dropin
     if not args.no_cpu:
         log(f"[bench] cpu baseline ({args.cpu_seconds:.0f} s budget)")
         # the chain is mostly single-threaded: the same rows on one thread and

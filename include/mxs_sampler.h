@@ -6,9 +6,9 @@
  *   -> softmax -> draw,
  * the chain of mini_engine/sampling.py:30-69, with per-row parameters passed
  * as device arrays.  Plain pointers and sizes only; every buffer belongs to
- * the caller and the library allocates nothing.  A call enqueues its kernels
- * (one; two for batches of up to 64 rows) on `stream` and returns; two calls
- * may run concurrently only with distinct workspaces.
+ * the caller and the library allocates nothing.  A call enqueues one kernel
+ * on `stream` and returns; two calls may run concurrently only with
+ * distinct workspaces.
  *
  * Results per row (token ids, post-filter probabilities) are defined by the
  * exact arithmetic described in the oracle that the tests check against:
@@ -68,11 +68,14 @@ const char* mxs_status_string(int status);
 
 /*
  * Workspace size in bytes for a batch of B rows of V logits (the same for
- * every valid shape, about 3 MB): batches of up to 64 rows first split each
- * row across several workgroups, which hand their candidates over in the
- * workspace; larger batches keep every row's state on chip.  It must be
- * 256-byte aligned; it needs no initialization and its contents need not
- * survive between calls.  Returns 0 for an invalid shape.
+ * every valid shape, about 3 MB): batches of up to 64 rows split each row
+ * across several workgroups, which hand their candidates over in the
+ * workspace and count themselves done on a per-row counter kept there;
+ * larger batches keep every row's state on chip.  It must be 256-byte
+ * aligned and zero-filled before its first use (every call returns the
+ * counters to zero, so a workspace is zero-filled once, not per call); its
+ * other contents need not survive between calls.  Returns 0 for an invalid
+ * shape.
  */
 size_t mxs_workspace_bytes(int B, int V);
 
@@ -100,7 +103,8 @@ size_t mxs_workspace_bytes(int B, int V);
  *   out_status    i32[B]  mxs_row_status per row, or NULL
  *   out_probs     f32[B, V] post-filter probabilities (sampling.py:68), or NULL.
  *                 Greedy rows get a one-hot row.
- *   workspace     device buffer of at least mxs_workspace_bytes(B, V) bytes
+ *   workspace     device buffer of at least mxs_workspace_bytes(B, V) bytes,
+ *                 zero-filled before its first use (see mxs_workspace_bytes)
  */
 int mxs_sample(const void* logits, int dtype, int B, int V, int64_t ld,
                const float* temperature, const int32_t* top_k,

@@ -1,4 +1,4 @@
-// k_f16_split.hip -- k_slices<__half> then k_fused<__half, true>: batches of up to SPLIT_MAX_B rows.
+// k_f16_split.hip -- k_split<__half>: batches of up to SPLIT_MAX_B rows, one launch.
 #include "sampler_kernels.h"
 
 namespace mxs {
@@ -6,14 +6,10 @@ namespace mxs {
 template <>
 hipError_t launch_split<__half>(const Params& p, hipStream_t s, bool& lds_error)
 {
-    static const hipError_t attr = hipFuncSetAttribute((const void*)k_fused<__half, true>,
+    static const hipError_t attr = hipFuncSetAttribute((const void*)k_split<__half>,
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, KF_LDS_BYTES);
     if (attr != hipSuccess) { lds_error = true; return attr; }
-    hipLaunchKernelGGL(k_slices<__half>, dim3((unsigned)p.G, (unsigned)p.B), dim3(NT), 0, s, p,
-                       (uint32_t*)p.sl_hdr, (uint32_t*)p.sl_ent);
-    const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((k_fused<__half, true>), dim3((unsigned)p.B), dim3(NT), KF_LDS_BYTES, s, p);
+    hipLaunchKernelGGL(k_split<__half>, dim3((unsigned)p.G, (unsigned)p.B), dim3(NT), KF_LDS_BYTES, s, p);
     return hipGetLastError();
 }
 

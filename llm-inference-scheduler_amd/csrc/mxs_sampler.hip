@@ -3,8 +3,8 @@
 //
 // Reference chain: mini_engine/sampling.py:30-69, one [vocab] row per call;
 // here one call samples a whole [B, V] batch.  Batches of more than
-// SPLIT_MAX_B rows run k_fused (one workgroup per row); smaller ones first
-// split their rows across workgroups with k_slices.
+// SPLIT_MAX_B rows run k_fused (one workgroup per row); smaller ones run
+// k_split, which splits their rows across workgroups.
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 #include <stddef.h>
@@ -20,8 +20,9 @@ using namespace mxs;
 namespace {
 
 // The workspace: k_fused keeps a row's state in LDS; the workspace holds
-// what k_slices hands over for batches of up to SPLIT_MAX_B rows (the same
-// size for every batch, so that a buffer sized once serves every batch).
+// what the slices of k_split hand over for batches of up to SPLIT_MAX_B
+// rows, and their per-row counters (the same size for every batch, so that
+// a buffer sized once serves every batch).
 constexpr size_t WORKSPACE_BYTES = (SL_WS_BYTES + 255) & ~(size_t)255;
 
 // mxs_sample_noalloc's workspace: a file-scope device array, one copy per

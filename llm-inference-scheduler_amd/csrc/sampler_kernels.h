@@ -2490,26 +2490,46 @@ __device__ __forceinline__ void sample_bound(const float (&sx)[NSAMP / NT], int 
 // ---------------------------------------------------------------- small batches
 //
 // With few rows, one workgroup per row leaves most CUs idle and each row's
-// stream runs at one CU's share of bandwidth.  For B <= SPLIT_MAX_B a first
-// kernel, k_slices, cuts every top-k row that can defer its penalty (and
-// every greedy row without one) into G slices of consecutive logits, one
-// workgroup per slice.  Every slice computes the row's sampled bound from
-// the same sample with the same code, so all slices agree on it; a slice
-// streams its logits and writes the keys that reach the bound with their
-// ids, its key extremes and the bound (a greedy slice: its packed maximum)
-// to a header and a candidate list in the workspace.  k_fused then loads a
-// row's candidates into its wave segments in place of its own stream and
-// goes on from the count pass; a row with a full slice, or one k_slices did
-// not take, streams in k_fused as usual.
+// stream runs at one CU's share of bandwidth.  For B <= SPLIT_MAX_B the
+// launch (k_split, at the end of this file) cuts every top-k row that can
+// defer its penalty (and every greedy row without one) into G slices of
+// consecutive logits, one workgroup per slice (slice_row).  Every slice
+// computes the row's sampled bound from the same sample with the same code,
+// so all slices agree on it; a slice streams its logits and writes the keys
+// that reach the bound with their ids, its key extremes and the bound (a
+// greedy slice: its packed maximum) to a header and a candidate list in the
+// workspace.  The row's last slice to finish then loads the row's
+// candidates into its wave segments in place of a stream of its own and
+// goes on from the count pass (fused_row); a row with a full slice, or one
+// the slices did not take, streams there as usual.
+
+// The slice's arrays: in the dynamic LDS of the launch, which the row's
+// finish (fused_row) reuses once every slice is done.
+constexpr int SL_LDS_HIST = 0;                                // 2048 bin counts
+constexpr int SL_LDS_CS = SL_LDS_HIST + 4 * 2048;             // 64 group sums
+constexpr int SL_LDS_N = SL_LDS_CS + 4 * 64;                  // the list's length
+constexpr int SL_LDS_KEY = SL_LDS_N + 16;                     // SLICE_CAP keys
+constexpr int SL_LDS_ID = SL_LDS_KEY + 4 * SLICE_CAP;         // SLICE_CAP ids
+static_assert(SL_LDS_ID + 4 * SLICE_CAP <= KF_LDS_BYTES, "a slice's arrays fit the row's LDS");
+
+// The hand-over is written with device-scope stores, which write through
+// this XCD's L2: once they are acknowledged, the row's finish (on any XCD)
+// reads them from memory after its acquire, and no L2 write-back is needed.
+__device__ __forceinline__ void put_dev(uint32_t* a, uint32_t v)
+{
+    __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 template <typename TIn>
-__global__ __launch_bounds__(NT, 1) void k_slices(Params p, uint32_t* hdr_all, uint32_t* ent_all)
+__device__ __forceinline__ void slice_row(const Params p, const int g, const int r, const int G, uint32_t* hdr_all,
+                                          uint32_t* ent_all, unsigned char* sm)
 {
-    __shared__ uint32_t s_hist[2048], s_cs[64];
-    __shared__ uint32_t s_key[SLICE_CAP], s_id[SLICE_CAP];
-    __shared__ uint32_t s_n;
+    uint32_t* s_hist = (uint32_t*)(sm + SL_LDS_HIST);
+    uint32_t* s_cs = (uint32_t*)(sm + SL_LDS_CS);
+    uint32_t& s_n = *(uint32_t*)(sm + SL_LDS_N);
+    uint32_t* s_key = (uint32_t*)(sm + SL_LDS_KEY);
+    uint32_t* s_id = (uint32_t*)(sm + SL_LDS_ID);
     const int tid = threadIdx.x, lane = lane_id();
-    const int G = (int)gridDim.x, g = (int)blockIdx.x, r = (int)blockIdx.y;
     const int V = p.V;
     const TIn* rowp = (const TIn*)p.logits + (size_t)r * (size_t)p.ld;
     uint32_t* hdr = hdr_all + (size_t)(r * G + g) * SL_HDR;
@@ -2528,7 +2548,7 @@ __global__ __launch_bounds__(NT, 1) void k_slices(Params p, uint32_t* hdr_all, u
     // (a greedy row with the LM head's maximum needs no slices)
     const bool greedy = mode == MODE_GREEDY && !pen_on && !p.pre_best;
     if ((!topk && !greedy) || hbad) {
-        if (tid == 0) hdr[0] = SL_NONE;
+        if (tid == 0) put_dev(hdr, SL_NONE);
         return;
     }
     // the slice: whole multiples of 8 logits (16-byte vectors of either dtype)
@@ -2545,7 +2565,7 @@ __global__ __launch_bounds__(NT, 1) void k_slices(Params p, uint32_t* hdr_all, u
             },
             [&](auto&&) { return false; });
         const u64 best = block_max<u64>(bk ? (((u64)bk << 32) | (u64)(0xFFFFFFFFu - bi)) : 0ull);
-        if (tid == 0) { hdr[5] = (uint32_t)best; hdr[6] = (uint32_t)(best >> 32); hdr[0] = 0; }
+        if (tid == 0) { put_dev(hdr + 5, (uint32_t)best); put_dev(hdr + 6, (uint32_t)(best >> 32)); put_dev(hdr, 0u); }
         return;
     }
     constexpr int NS = NSAMP / NT;
@@ -2594,13 +2614,15 @@ __global__ __launch_bounds__(NT, 1) void k_slices(Params p, uint32_t* hdr_all, u
     const Reduced rd = block_reduce(omax, omin, 0u);   // (its barriers publish the list)
     const uint32_t nh = s_n;
     if (nh <= (uint32_t)SLICE_CAP)
-        for (uint32_t j = (uint32_t)tid; j < nh; j += NT) { ent[2 * j] = s_key[j]; ent[2 * j + 1] = s_id[j]; }
+        for (uint32_t j = (uint32_t)tid; j < nh; j += NT)
+            __hip_atomic_store((u64*)ent + j, (u64)s_key[j] | ((u64)s_id[j] << 32), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
     if (tid == 0) {
-        hdr[0] = nh <= (uint32_t)SLICE_CAP ? nh : SL_NONE;
-        hdr[1] = rd.max;
-        hdr[2] = rd.min;
-        hdr[3] = est;
-        hdr[4] = theta;
+        put_dev(hdr, nh <= (uint32_t)SLICE_CAP ? nh : SL_NONE);
+        put_dev(hdr + 1, rd.max);
+        put_dev(hdr + 2, rd.min);
+        put_dev(hdr + 3, est);
+        put_dev(hdr + 4, theta);
     }
 }
 
@@ -2633,12 +2655,12 @@ __device__ __forceinline__ bool finish_counts_as(const Params& p, int r, RowStre
     }
 }
 
-// SPLIT: the launch follows k_slices (small batches), whose candidates may
-// replace a row's stream; the instance without it has none of that code.
+// One row's chain in one workgroup.  SPLIT: the row's slices (slice_row)
+// are done, and their candidates may replace the row's stream; the
+// instance without it has none of that code.
 template <typename TIn, bool SPLIT>
-__global__ __launch_bounds__(NT, 1) void k_fused(Params p)
+__device__ __forceinline__ void fused_row(const Params p, const int r, unsigned char* smem)
 {
-    extern __shared__ __align__(16) unsigned char smem[];
     uint32_t* ck = (uint32_t*)(smem + KF_CK);   // candidate selection keys
     uint32_t* ci = (uint32_t*)(smem + KF_CI);   // candidate ids
     uint32_t* bm = (uint32_t*)(smem + KF_BM);   // history bitmap
@@ -2651,7 +2673,6 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
     __shared__ uint32_t s_cs[64];               // counts per group of 32 bins
 
     const int tid = threadIdx.x, lane = lane_id();
-    const int r = blockIdx.x;
     const int V = p.V;
     const TIn* rowp = (const TIn*)p.logits + (size_t)r * (size_t)p.ld;
     // Loads are issued in the order they are needed: the row's parameters,
@@ -2671,20 +2692,25 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
     pa = (lane == 5 && p.hoff) ? (const uint32_t*)(p.hend ? p.hend + r : p.hoff + r + 1) : pa;
     pa = (lane == 6 && p.U) ? (const uint32_t*)(p.U + r) : pa;
     const uint32_t pv = *pa;
-    // k_slices' slice headers of this row (a slice count per lane)
+    // the slice headers of this row (a slice count per lane)
     uint32_t sln = 0;
     if constexpr (SPLIT) sln = p.sl_hdr[(size_t)(r * p.G + (lane < p.G ? lane : 0)) * SL_HDR];
     // The sample: NSAMP logits in 64 groups of 32 consecutive ones spread
     // over the row (a group is one 128-byte line of an fp32 row), 4 per
     // thread.  It is requested before the row's mode is known, so that it
     // does not queue behind the tiles; rows that do not use it waste 8 KB.
+    // (After the slices it is requested only for a row they did not take:
+    // the hand-over's loads would otherwise wait behind it.)
     constexpr int NS = NSAMP / NT;
     static_assert(NSAMP == 64 * 32 && NS * 8 == 32, "sample layout");
     float sx[NS];
     const int se0 = (((tid >> 3) * (V >> 6)) & ~31) + (tid & 7) * NS;   // this thread's first sample
+    auto load_sample = [&]() {
 #pragma unroll
-    for (int q = 0; q < NS; ++q) sx[q] = VecIO<TIn>::one(rowp, se0 + q < V ? se0 + q : V - 1);
-    // (after k_slices, or with the LM head's maxima: issued later, for the rows that stream)
+        for (int q = 0; q < NS; ++q) sx[q] = VecIO<TIn>::one(rowp, se0 + q < V ? se0 + q : V - 1);
+    };
+    if constexpr (!SPLIT) load_sample();
+    // (after the slices, or with the LM head's maxima: issued later, for the rows that stream)
     const bool early = !SPLIT && !p.pre_best;
     RowStream<TIn> rs(rowp, V, early);
     __builtin_amdgcn_sched_barrier(0);   // (the loads above stay ahead of the reads below)
@@ -2702,7 +2728,10 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
     RowMode mode = classify(T, k, V);
     // every slice of the row handed over its part: the candidates replace the stream
     bool split = false;
-    if constexpr (SPLIT) split = !__ballot(lane < p.G && sln == SL_NONE);
+    if constexpr (SPLIT) {
+        split = !__ballot(lane < p.G && sln == SL_NONE);
+        if (!split) load_sample();
+    }
     const bool neg = T < 0.0f;
     const bool pen_on = (pen != 1.0f) && (h1 > h0);
     // a greedy row without a penalty takes the LM head's maximum (sampling.py:47-48)
@@ -2944,7 +2973,7 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
             //    k * NSAMP / V.  It only steers the stream; step 3 checks it.
             //    (Computed before the row modes branch, as est0 / theta0.)
             bool fast = sampled;
-            if (fast && split) {   // k_slices computed the same bound
+            if (fast && split) {   // the slices computed the same bound
                 est = p.sl_hdr[(size_t)r * p.G * SL_HDR + 3];
                 theta = p.sl_hdr[(size_t)r * p.G * SL_HDR + 4];
                 __syncthreads();   // (s_ovf is cleared before any wave may set it)
@@ -2963,22 +2992,44 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                 constexpr uint32_t SEG_USE = FSEG - 64;   // [SEG_USE, FSEG): the dummy words
                 if (split) {
                     // the candidates of slices w, w + NWAVES, ... into this wave's
-                    // segment: the slices' headers one per lane, their offsets by
-                    // a wave prefix, then the entries eight loads per lane at a
-                    // time (clamped indices: no load behind a branch)
-                    const int nsw = w < p.G ? (p.G - w + NWAVES - 1) / NWAVES : 0;   // (<= 64 / NWAVES)
+                    // segment: the slices' headers one per lane and, in the same
+                    // round trip, entry `lane` of each of the wave's slices (most
+                    // slices hand over fewer than 64); then the offsets by a wave
+                    // prefix.  A slice with more than 64 takes the general loop,
+                    // eight loads per lane at a time (clamped indices: no load
+                    // behind a branch).
+                    constexpr int SPW = 64 / NWAVES;   // slices per wave at most (G <= 64)
+                    static_assert(SPW * NWAVES == 64, "every slice has a wave");
+                    const int nsw = w < p.G ? (p.G - w + NWAVES - 1) / NWAVES : 0;   // (<= SPW)
                     const int gh = w + NWAVES * (lane < nsw ? lane : 0);   // (a wave without slices reads slice G - 1)
                     const uint32_t* h = p.sl_hdr + (size_t)(r * p.G + (gh < p.G ? gh : p.G - 1)) * SL_HDR;
                     const bool mine = lane < nsw;
                     const uint32_t hn = h[0], hmx = h[1], hmn = h[2];
+                    uint2 sp[SPW];
+#pragma unroll
+                    for (int i = 0; i < SPW; ++i) {
+                        const int si = w + NWAVES * (i < nsw ? i : 0);
+                        sp[i] = ((const uint2*)(p.sl_ent + (size_t)(r * p.G + (si < p.G ? si : p.G - 1)) * SLICE_CAP * 2))[lane];
+                    }
                     const uint32_t ng = mine ? hn : 0u;
                     omax = wave_max_u32(mine ? hmx : 0u);
                     omin = wave_min_u32(mine ? hmn : 0xFFFFFFFFu);
                     const uint32_t incl = wave_prefix_u32(ng);
                     const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
                     const uint32_t excl = incl - ng;
+                    const bool small = wave_max_u32(ng) <= 64u;
                     if (total > SEG_USE) {
                         if (lane == 0) __hip_atomic_store(&s_ovf, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                    } else if (small) {
+#pragma unroll
+                        for (int i = 0; i < SPW; ++i) {
+                            if (i < nsw) {
+                                const uint32_t ni = (uint32_t)__builtin_amdgcn_readlane((int)ng, i);
+                                const uint32_t ei = (uint32_t)__builtin_amdgcn_readlane((int)excl, i);
+                                if ((uint32_t)lane < ni) { wck[ei + lane] = sp[i].x; wci[ei + lane] = sp[i].y; }
+                            }
+                        }
+                        cw = total;
                     } else {
                         for (uint32_t q0 = 0; q0 < total; q0 += 512u) {
                             uint2 v[8];
@@ -3111,7 +3162,7 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
                     for (int q = 0; q < 4; ++q) {
                         const uint32_t j = j0 + 64u * q;
                         if (j >= cw) continue;
-                        // (the stream left raw values; k_slices' candidates are keys)
+                        // (the stream left raw values; the slices' candidates are keys)
                         float x = split ? sel_inv(key[q], neg) : u2f(key[q]);
                         const bool hp = (bw[q] >> (id[q] & 31)) & 1u;
                         if (hp) x = penalize(x, pen);
@@ -3391,6 +3442,49 @@ __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
         p.out_tok[r] = st == MXS_ROW_OK ? tok : -1;
         if (p.out_status) p.out_status[r] = st;
     }
+}
+
+// Batches above SPLIT_MAX_B rows: one workgroup per row.
+template <typename TIn>
+__global__ __launch_bounds__(NT, 1) void k_fused(Params p)
+{
+    extern __shared__ __align__(16) unsigned char smem[];
+    fused_row<TIn, false>(p, (int)blockIdx.x, smem);
+}
+
+// Batches of up to SPLIT_MAX_B rows, in one launch: workgroup (g, r) runs
+// slice g of row r, and the row's last slice to finish (one counter per
+// row in the workspace, zero before the launch, which that workgroup
+// returns to zero) goes on with the row's chain from the slices'
+// hand-over.  No workgroup waits for another.  The hand-over is written
+// through to memory (put_dev) and every wave waits until its stores are
+// acknowledged before the count (a release fence would also write back
+// this XCD's whole L2, about a microsecond); in the last workgroup one
+// thread acquires the other slices' writes after it (invalidating the
+// caches its waves read through).
+template <typename TIn>
+__global__ __launch_bounds__(NT, 1) void k_split(Params p)
+{
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ uint32_t s_last;
+    const int G = (int)gridDim.x, g = (int)blockIdx.x, r = (int)blockIdx.y;
+    slice_row<TIn>(p, g, r, G, (uint32_t*)p.sl_hdr, (uint32_t*)p.sl_ent, smem);
+    __builtin_amdgcn_s_waitcnt(0);   // (all counters: this wave's stores are acknowledged)
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        // the counter: the unused last word of the header of the row's slice 0
+        uint32_t* cnt = (uint32_t*)p.sl_hdr + (size_t)r * G * SL_HDR + SL_CNT_WORD;
+        const uint32_t before = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = before == (uint32_t)(G - 1);
+        if (last) {
+            __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        }
+        s_last = last ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    fused_row<TIn, true>(p, r, smem);
 }
 
 }  // namespace

@@ -29,7 +29,7 @@ struct Params {
     int64_t* out_tok;
     int32_t* out_status;
     float* out_probs;
-    // candidates handed over by k_slices (NULL: none): G slices per row
+    // candidates handed over by the slices of k_split (NULL: none): G slices per row
     const uint32_t* sl_hdr;
     const uint32_t* sl_ent;
     int G;
@@ -40,14 +40,15 @@ struct Params {
 
 // ---------------------------------------------------------------- small batches
 //
-// For B <= SPLIT_MAX_B every row that k_slices takes is cut into G slices of
-// consecutive logits, one workgroup each; each slice hands its candidates
-// to k_fused through the workspace: a header of SL_HDR words and up to
-// SLICE_CAP (key, id) pairs per slice.
+// For B <= SPLIT_MAX_B every row that slice_row takes is cut into G slices
+// of consecutive logits, one workgroup each (k_split); each slice hands its
+// candidates to the row's finish through the workspace: a header of SL_HDR
+// words and up to SLICE_CAP (key, id) pairs per slice.
 constexpr int SPLIT_MAX_B = 64;
 constexpr int SPLIT_SLICES = 256;              // B * G at most
 constexpr int SLICE_CAP = FSEG - 64;           // candidates of one slice (a wave segment's room)
 constexpr int SL_HDR = 8;                      // header words: n, key max, key min, est, theta, best lo, best hi
+constexpr int SL_CNT_WORD = 7;                 // slice 0's last header word: the row's count of finished slices
 constexpr uint32_t SL_NONE = 0xFFFFFFFFu;      // n of a slice that hands over nothing
 constexpr size_t SL_HDR_BYTES = (size_t)SPLIT_SLICES * SL_HDR * 4;
 constexpr size_t SL_WS_BYTES = SL_HDR_BYTES + (size_t)SPLIT_SLICES * SLICE_CAP * 8;

@@ -48,13 +48,14 @@ _workspaces: dict = {}
 
 def workspace(device: torch.device, B: int, V: int) -> torch.Tensor:
     """A workspace of at least mxs_workspace_bytes(B, V) bytes for `device`
-    and its current stream (one per (device, stream), grown on demand).  The
-    kernels need it neither zeroed nor preserved between calls."""
+    and its current stream (one per (device, stream), grown on demand),
+    zero-filled when allocated: the small-batch launch keeps one counter per
+    row in it, which every call returns to zero."""
     need = int(extension().workspace_bytes(B, V))
     stream = torch.cuda.current_stream(device)
     key = (device.index, stream.cuda_stream)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < need:
-        ws = torch.empty(max(need, 256), dtype=torch.uint8, device=device)
+        ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=device)
         _workspaces[key] = ws
     return ws

@@ -78,8 +78,8 @@ class Sampler:
         self.status = torch.empty(B, dtype=torch.int32, device=self.device)
         self.probs = (torch.zeros((B, V), dtype=torch.float32, device=self.device)
                       if with_probs else None)
-        self.workspace = torch.empty(max(int(self.ext.workspace_bytes(B, V)), 256),
-                                     dtype=torch.uint8, device=self.device)
+        self.workspace = torch.zeros(max(int(self.ext.workspace_bytes(B, V)), 256),
+                                     dtype=torch.uint8, device=self.device)   # (zero-filled once)
 
     def run(self, logits, temperature, top_k, top_p, penalty, hist_offsets=None,
             hist_ids=None, uniforms=None):

@@ -19,8 +19,10 @@ Documented differences from the reference:
 
 from __future__ import annotations
 
+import threading
 from dataclasses import dataclass, field
 
+import numpy as np
 import torch
 
 from . import _native
@@ -42,6 +44,42 @@ class SamplingParams:
         return self.temperature == 0.0
 
 
+class _RowBuffers:
+    """Per-device buffers of the one-row call, made once: a pinned host
+    block and its device copy (parameters, CSR offsets and the history ids),
+    the device outputs and a pinned block they come back to, and the
+    tensor views the extension takes (so a call makes no new tensors)."""
+
+    def __init__(self, device: torch.device, n: int):
+        self.n = n
+        self.lock = threading.Lock()   # (one call at a time uses the blocks)
+        self.pin_in = torch.empty(8 + n, dtype=torch.int32, pin_memory=True)
+        self.host = self.pin_in.numpy()
+        self.host_f = self.host.view(np.float32)
+        self.dev_in = torch.empty(8 + n, dtype=torch.int32, device=device)
+        f = self.dev_in.view(torch.float32)
+        self.T, self.K, self.P, self.PEN, self.U = f[0:1], self.dev_in[1:2], f[2:3], f[3:4], f[4:5]
+        self.off, self.ids = self.dev_in[5:7], self.dev_in[8:]
+        self.dev_out = torch.empty(2, dtype=torch.int64, device=device)   # token, then the status word
+        self.tokens = self.dev_out[0:1]
+        self.status = self.dev_out[1:2].view(torch.int32)[0:1]
+        self.pin_out = torch.empty(2, dtype=torch.int64, pin_memory=True)
+        self.out = self.pin_out.numpy()
+
+
+_row_buffers: dict = {}
+_row_buffers_lock = threading.Lock()
+
+
+def _buffers(device: torch.device, H: int) -> _RowBuffers:
+    with _row_buffers_lock:
+        b = _row_buffers.get(device.index)
+        if b is None or b.n < max(H, 1):
+            b = _RowBuffers(device, max(H, 1024))
+            _row_buffers[device.index] = b
+        return b
+
+
 def sample(
     logits: torch.Tensor,  # [vocab]
     params: SamplingParams,
@@ -53,7 +91,10 @@ def sample(
     Logits on the CPU are copied to the current GPU first (the copy crosses
     PCIe; keep logits on the device to avoid it).  float32 and float16 rows
     are read as they are; other dtypes are upcast to float32 first, as
-    `logits.float()` does at sampling.py:36.
+    `logits.float()` does at sampling.py:36.  The parameters and history go
+    over in one asynchronous copy from a pinned block, and the token and
+    status come back in one: the call synchronizes once, as `.item()` does
+    at sampling.py:69.
     """
     if logits.dim() != 1:
         raise ValueError(f"sample() takes one [vocab] row, got shape {tuple(logits.shape)}")
@@ -75,26 +116,35 @@ def sample(
         u = float(torch.rand((), generator=generator))
 
     H = len(hist)
-    buf = torch.empty(8 + max(H, 1), dtype=torch.int32)
-    f = buf.view(torch.float32)
-    f[0] = device_temperature(params.temperature)
+    b = _buffers(x.device, H)
+    with b.lock:
+        return _sample_row(ext, x, b, params, hist, u)
+
+
+def _sample_row(ext, x, b: _RowBuffers, params: SamplingParams, hist: list, u: float) -> int:
+    H = len(hist)
+    V = x.shape[0]
+    h, hf = b.host, b.host_f
+    hf[0] = device_temperature(params.temperature)
     tk = int(params.top_k)
-    buf[1] = tk if -2**31 <= tk < 2**31 else 2**31 - 1
-    f[2] = float(params.top_p)
-    f[3] = float(params.repetition_penalty)
-    f[4] = u
-    buf[5] = 0
-    buf[6] = H
+    h[1] = tk if -2**31 <= tk < 2**31 else 2**31 - 1
+    hf[2] = float(params.top_p)
+    hf[3] = float(params.repetition_penalty)
+    hf[4] = u
+    h[5] = 0
+    h[6] = H
     if H:
-        buf[8:8 + H] = torch.tensor(hist, dtype=torch.int32)
-    d = buf.to(x.device)
-    df = d.view(torch.float32)
-    tokens = torch.empty(1, dtype=torch.int64, device=x.device)
-    status = torch.empty(1, dtype=torch.int32, device=x.device)
-    ws = _native.workspace(x.device, 1, V)
-    ext.sample(x.unsqueeze(0), df[0:1], d[1:2], df[2:3], df[3:4],
-               d[5:7], d[8:8 + H], df[4:5], tokens, status, None, ws)
-    tok, st = torch.cat([tokens, status.to(torch.int64)]).tolist()   # one sync, as .item() at :69
+        h[8:8 + H] = hist
+    stream = torch.cuda.current_stream(x.device)
+    try:
+        b.dev_in[:8 + H].copy_(b.pin_in[:8 + H], non_blocking=True)
+        ws = _native.workspace(x.device, 1, V)
+        ext.sample(x.unsqueeze(0), b.T, b.K, b.P, b.PEN, b.off, b.ids, b.U, b.tokens, b.status, None, ws)
+        b.pin_out.copy_(b.dev_out, non_blocking=True)
+    finally:
+        stream.synchronize()   # (also before the pinned blocks may be written again)
+    tok = int(b.out[0])
+    st = int(b.out[1] & 0xFFFFFFFF)
     if st != ROW_OK:
         raise_row_status(st)
     return tok

@@ -206,7 +206,7 @@ def test_ctypes_binding_launch(oracle, cuda, name):
     B, V = w.B, w.V
     tok = torch.empty(B, dtype=torch.int64, device=cuda)
     st = torch.empty(B, dtype=torch.int32, device=cuda)
-    ws = torch.empty(lib.mxs_workspace_bytes(B, V), dtype=torch.uint8, device=cuda)
+    ws = torch.zeros(lib.mxs_workspace_bytes(B, V), dtype=torch.uint8, device=cuda)
     stream = torch.cuda.current_stream(cuda).cuda_stream
     say(f"[scheduler] ctypes launch {name}")
     x = d["logits"]

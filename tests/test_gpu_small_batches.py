@@ -1,7 +1,7 @@
-"""Batches of up to 64 rows go through k_slices (each top-k row with a
+"""Batches of up to 64 rows go through k_split (each top-k row with a
 deferrable penalty, and each greedy row without one, cut into up to 64
-slices that hand their candidates over) before k_fused.  Cases where the
-hand-over must give way: a slice with more candidates than it can hold,
+slices that hand their candidates over; the row's last slice to finish
+runs the rest of the chain).  Cases where the hand-over must give way: a slice with more candidates than it can hold,
 a bound that fails (heavy ties), NaN inside one slice, rows it does not take
 (penalty below 1, T < 0, top-k off, k above the candidate cap), odd vocab
 sizes whose last slices are short or empty, and unaligned fp16 rows.
@@ -77,3 +77,41 @@ def test_split_batches_match_the_oracle(oracle, cuda, B, V, dtype):
         assert np.array_equal(st.cpu().numpy(), ref.status)
         assert np.array_equal(tok.cpu().numpy(), ref.tokens), (tok.cpu().numpy(), ref.tokens)
         assert np.abs(probs.cpu().numpy() - ref.probs).max() <= 1e-6
+
+
+def test_counters_return_to_zero_across_batch_sizes(oracle, cuda):
+    """One workspace for a sequence of batch sizes (the slice count G, and
+    with it where each row's counter lives, changes from call to call):
+    every call matches the oracle, and afterwards every counter word (the
+    last word of each slice header) is zero again, as the next call needs."""
+    import ctypes
+    import os
+    root = os.path.abspath(os.path.join(os.path.dirname(__file__), ".."))
+    lib = ctypes.CDLL(os.path.join(root, "llm-inference-scheduler_amd", "mi355x_sampler", "_lib",
+                                   "libmxs_sampler.so"))
+    lib.mxs_workspace_bytes.restype = ctypes.c_size_t
+    lib.mxs_workspace_bytes.argtypes = [ctypes.c_int, ctypes.c_int]
+    P = ctypes.c_void_p
+    lib.mxs_sample.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int64, P, P, P, P, P, P,
+                               ctypes.c_int64, P, P, P, P, P, ctypes.c_size_t, P]
+    V = VOCAB
+    ws = torch.zeros(lib.mxs_workspace_bytes(64, V), dtype=torch.uint8, device=cuda)
+    for i, B in enumerate([1, 3, 64, 5, 64, 2, 17, 1]):
+        w = batch(B, V, 100 + i)
+        say(f"[counters] call {i} B={B}")
+        d = w.to_device(cuda)
+        tok = torch.empty(B, dtype=torch.int64, device=cuda)
+        st = torch.empty(B, dtype=torch.int32, device=cuda)
+        rc = lib.mxs_sample(d["logits"].data_ptr(), 0, B, V, V, d["temperature"].data_ptr(), d["top_k"].data_ptr(),
+                            d["top_p"].data_ptr(), d["penalty"].data_ptr(), d["hist_offsets"].data_ptr(),
+                            d["hist_ids"].data_ptr(), d["hist_ids"].numel(), d["uniforms"].data_ptr(),
+                            tok.data_ptr(), st.data_ptr(), None, ws.data_ptr(), ws.numel(),
+                            P(torch.cuda.current_stream().cuda_stream))
+        assert rc == 0
+        torch.cuda.synchronize()
+        ref = oracle.sample_rows(w.logits, w.temperature, w.top_k, w.top_p, w.penalty,
+                                 w.hist_offsets, w.hist_ids, w.uniforms)
+        assert np.array_equal(st.cpu().numpy(), ref.status)
+        assert np.array_equal(tok.cpu().numpy(), ref.tokens)
+        headers = ws[: 256 * 8 * 4].view(torch.int32).view(256, 8).cpu().numpy()
+        assert (headers[:, 7] == 0).all(), np.nonzero(headers[:, 7])[0]

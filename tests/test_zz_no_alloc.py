@@ -55,7 +55,7 @@ def launch(lib, w, d, cuda, noalloc):
     if noalloc:
         rc = lib.mxs_sample_noalloc(*args, stream)
     else:
-        ws = torch.empty(lib.mxs_workspace_bytes(B, V), dtype=torch.uint8, device=cuda)
+        ws = torch.zeros(lib.mxs_workspace_bytes(B, V), dtype=torch.uint8, device=cuda)
         rc = lib.mxs_sample(*args, ws.data_ptr(), ws.numel(), stream)
     assert rc == 0, lib.mxs_status_string(rc).decode()
     torch.cuda.synchronize()
