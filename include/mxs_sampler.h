@@ -68,10 +68,13 @@ const char* mxs_status_string(int status);
 
 /*
  * Workspace size in bytes for a batch of B rows of V logits (the same for
- * every valid shape, about 3 MB): batches of up to 64 rows split each row
+ * every valid shape, about 4.3 MiB): batches of up to 64 rows split each row
  * across several workgroups, which hand their candidates over in the
  * workspace and count themselves done on a per-row counter kept there;
- * larger batches keep every row's state on chip.  It must be 256-byte
+ * larger batches keep every row's state on chip, and a row with top-k off
+ * hands slices of its passes to workgroups that finished their own rows
+ * through job records kept there (tagged with the call, so never reset).
+ * It must be 256-byte
  * aligned and zero-filled before its first use (every call returns the
  * counters to zero, so a workspace is zero-filled once, not per call); its
  * other contents need not survive between calls.  Returns 0 for an invalid
@@ -188,7 +191,7 @@ int mxs_sample_head(const void* logits, int dtype, int B, int V, int64_t ld,
  * GPU (different streams, or different threads) race and must be
  * serialized by the caller.  Arguments and results are as for mxs_sample.
  */
-#define MXS_NOALLOC_SCRATCH_BYTES 3022848
+#define MXS_NOALLOC_SCRATCH_BYTES 4501504
 int mxs_sample_noalloc(const void* logits, int dtype, int B, int V, int64_t ld,
                        const float* temperature, const int32_t* top_k,
                        const float* top_p, const float* penalty,

@@ -315,7 +315,7 @@ struct BinHit {
 // Descending search over h[0..nb): the bin b with  above(b) <= t < above(b) + h[b],
 // where above(b) = sum of h over bins > b.  nb must be a multiple of NT.
 template <typename T>
-__device__ BinHit find_desc(const T* h, int nb, u64 t)
+__device__ __forceinline__ BinHit find_desc(const T* h, int nb, u64 t)
 {
     __shared__ BinHit s_hit;
     const int per = nb / NT;
@@ -344,7 +344,7 @@ __device__ BinHit find_desc(const T* h, int nb, u64 t)
 // holding the answer has at most `small` keys the search stops and returns
 // that bin's lower edge (a valid lower bound); small = 0 gives the exact key.
 template <class Visit>
-__device__ uint32_t block_select_desc_v(uint32_t kk, Visit visit, uint32_t* hist, uint32_t small)
+__device__ __forceinline__ uint32_t block_select_desc_v(uint32_t kk, Visit visit, uint32_t* hist, uint32_t small)
 {
     const int shifts[3] = {21, 10, 0};
     const int widths[3] = {11, 11, 10};
@@ -370,7 +370,7 @@ __device__ uint32_t block_select_desc_v(uint32_t kk, Visit visit, uint32_t* hist
 
 // Indexed form: keys key(i) for i in [0, n).
 template <class KeyF>
-__device__ uint32_t block_select_desc(int n, uint32_t kk, KeyF key, uint32_t* hist, uint32_t small)
+__device__ __forceinline__ uint32_t block_select_desc(int n, uint32_t kk, KeyF key, uint32_t* hist, uint32_t small)
 {
     return block_select_desc_v(kk, [&](auto&& f) {
         for (int i = threadIdx.x; i < n; i += NT) f(key(i));

@@ -10,6 +10,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "mxs_sampler.h"
@@ -23,7 +24,8 @@ namespace {
 // what the slices of k_split hand over for batches of up to SPLIT_MAX_B
 // rows, and their per-row counters (the same size for every batch, so that
 // a buffer sized once serves every batch).
-constexpr size_t WORKSPACE_BYTES = (SL_WS_BYTES + 255) & ~(size_t)255;
+constexpr size_t WJ_OFF = (SL_WS_BYTES + 255) & ~(size_t)255;   // the shared-row records
+constexpr size_t WORKSPACE_BYTES = (WJ_OFF + WJ_BYTES + 255) & ~(size_t)255;
 
 // mxs_sample_noalloc's workspace: a file-scope device array, one copy per
 // GPU (each holds it from the library's load to the process's end).  Host
@@ -51,6 +53,28 @@ int scratch_of_current_device(void** out)
     *out = g_scratch_ptr[dev];
     return MXS_OK;
 }
+
+// The current device's compute-unit count (looked up once per device): a
+// batch of at most that many rows has every row's workgroup resident from
+// the start, the condition for workgroups to wait for shared rows' slices.
+int cus_of_current_device()
+{
+    static std::mutex mu;
+    static int cus[SCRATCH_MAX_DEVICES];
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= SCRATCH_MAX_DEVICES) return 0;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!cus[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+// Each call's epoch, which tags its shared-row records (never 0, the value
+// of a zero-filled workspace).
+std::atomic<unsigned int> g_epoch{0};
 
 }  // namespace
 
@@ -127,11 +151,22 @@ int sample_impl(const void* logits, int dtype, int B, int V, int64_t ld,
     p.sl_hdr = nullptr;
     p.sl_ent = nullptr;
     p.G = 0;
+    p.wj = nullptr;
+    p.epoch = 0;
+    p.help = 0;
+    p.wown = (unsigned int*)((unsigned char*)workspace + WJ_OFF + WJ_NJOB * WJ_JOB_BYTES);
     hipStream_t s = (hipStream_t)stream;
     if (B <= SPLIT_MAX_B) {
         p.G = split_slices(B);
         p.sl_hdr = (const uint32_t*)workspace;
         p.sl_ent = (const uint32_t*)((const char*)workspace + SL_HDR_BYTES);
+    } else {
+        p.wj = (unsigned char*)workspace + WJ_OFF;
+        unsigned int e = ++g_epoch;
+        if (e == 0) e = ++g_epoch;
+        p.epoch = e;
+        const int cus = cus_of_current_device();
+        p.help = cus > 0 && B <= cus ? 1 : 0;
     }
     bool lds_error = false;
     hipError_t e;

@@ -1024,6 +1024,15 @@ struct RowStream {
         ntile = (nvec + TV - 1) / TV;
         restart(issue);
     }
+    // The stream of another range of logits (the first two tiles issued).
+    __device__ __forceinline__ void retarget(const TIn* rp, int v)
+    {
+        rowp = rp;
+        V = v;
+        nvec = ((((uintptr_t)rp) & 15u) == 0) ? v / VW : 0;
+        ntile = (nvec + TV - 1) / TV;
+        restart();
+    }
     // The first two tiles.  The tile numbers pass through an empty asm
     // statement, so that the compiler computes these addresses at each use
     // instead of keeping one set alive (in scratch) for all the passes.
@@ -1607,19 +1616,302 @@ constexpr int W2_KD = KF_CK + 8 * LCAP;  //         the draw's window (LCAP u64)
 constexpr int W2_SMH = KF_CK + 16 * LCAP;   // pick_in_set's masses (2048 u64)
 static_assert(W2_SMH + 16384 <= KF_HL, "the windows and pick_in_set's masses fit below the history list");
 static_assert(TL_CAP * 8 <= KF_H - KF_MH, "the top list fits where the mass histogram was");
+static_assert(WJ_TOP == TL_CAP && WJ_WIN == LCAP, "a job's lists hold what the owner's do");
+constexpr uint32_t W2_SEG_USE = FSEG - 64;   // a wave segment's room (the rest: dummy slots)
 
-template <typename TIn>
+// ---- shared rows: the records (sampler_params.h has their layout)
+//
+// A pass of a shared row is cut into S slices of tps tiles (S <= WJ_S).  The
+// owner streams the row from its first tile and claims the slices from the
+// front, each one two tiles before it reaches it (so the claim's round trip
+// hides behind the stream); helpers claim from the back.  Both claims are
+// additions to one word per pass, (back << 16) | front: a claim is granted
+// when front + back < S before it, so the first S claims, in the word's
+// order, take every slice exactly once (the owner's [0, taken), the
+// helpers' [taken, S)) and every later claim is refused.
+struct WideJob {
+    u64 tag;                          // (epoch << 32) | (WJ_MAGIC << 16) | (S << 8) | phase (1, 2 open; 3 closed)
+    uint32_t own;                     // the epoch of the call whose row holds the slot
+    uint32_t tps;                     // tiles per slice
+    uint32_t q1, q2;                  // the claims of pass 1 and pass 2 (adjacent: one 64-bit read)
+    uint32_t done1, done2;            // slices of each pass finished by helpers
+    int r, h0, h1, pad0;              // the row, its history
+    float T, pen, yhi, ylo, scale, m, yca, ycb, yda, ydb;
+    uint32_t neg, pen_on;
+    uint32_t gmax, gmin;              // pass 1: the helpers' key extremes
+    uint32_t ntop, ovf;               // pass 1: their top-list entries; a list or segment ran full
+    uint32_t nc, nd;                  // pass 2: their window elements
+    u64 wb, ac, ad;                   // pass 2: their sums
+};
+static_assert(sizeof(WideJob) <= WJ_HDR, "a job's header");
+static_assert(WJ_S < 256 && WJ_NJOB <= 64, "S fits the tag; one lane per job");
+constexpr uint32_t WJ_MAGIC = 0xA5C7u;
+constexpr int WJ_SPIN = 1 << 21;      // bounded waits: polls of about 50 ns each
+
+__device__ __forceinline__ WideJob* wj_job(unsigned char* wj, int j) { return (WideJob*)(wj + (size_t)j * WJ_JOB_BYTES); }
+// a word of workgroup (or row) r's own, which its unshared passes read (a
+// line each; beyond WJ_OWN they share)
+__device__ __forceinline__ uint32_t* wj_own_word(const Params& p, int r) { return p.wown + (size_t)(r % WJ_OWN) * 16; }
+__device__ __forceinline__ uint32_t* wj_bins(WideJob* J) { return (uint32_t*)((unsigned char*)J + WJ_HDR); }
+__device__ __forceinline__ u64* wj_top(WideJob* J) { return (u64*)(wj_bins(J) + 2048); }
+__device__ __forceinline__ u64* wj_kc(WideJob* J) { return wj_top(J) + WJ_TOP; }
+__device__ __forceinline__ u64* wj_kd(WideJob* J) { return wj_kc(J) + WJ_WIN; }
+__device__ __forceinline__ u64 wj_tag(uint32_t epoch, int S, uint32_t phase)
+{
+    return ((u64)epoch << 32) | ((u64)WJ_MAGIC << 16) | ((u64)S << 8) | phase;
+}
+// device-scope accesses of the records (they bypass a stale copy in this
+// XCD's caches; stores write through, see put_dev)
+__device__ __forceinline__ uint32_t ld_dev(const uint32_t* a)
+{
+    return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ u64 ld_dev64(const u64* a) { return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ float ld_devf(const float* a) { return u2f(ld_dev((const uint32_t*)a)); }
+__device__ __forceinline__ void put_dev32(uint32_t* a, uint32_t v)
+{
+    __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void put_dev64(u64* a, u64 v) { __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ void put_devf(float* a, float v) { put_dev32((uint32_t*)a, f2u(v)); }
+
+// The batch's rows with top-k off among its first NT rows, a bit per row,
+// wave w's ballot over rows [64 w, 64 w + 64) at the start of fused_row
+// (k_fused): their count, and a row's rank among them.
+__shared__ u64 g_wide[NWAVES];
+__device__ __forceinline__ uint32_t wide_rows_counted()
+{
+    uint32_t n = 0;
+#pragma unroll
+    for (int v = 0; v < NWAVES; ++v) n += (uint32_t)__builtin_popcountll(g_wide[v]);
+    return n;
+}
+__device__ __forceinline__ int wide_rank(int r)
+{
+    int n = 0;
+#pragma unroll
+    for (int v = 0; v < NWAVES; ++v) {
+        const u64 m = g_wide[v];
+        n += v < (r >> 6) ? __builtin_popcountll(m) : 0;
+        n += v == (r >> 6) ? __builtin_popcountll(m & ((1ull << (r & 63)) - 1ull)) : 0;
+    }
+    return n;
+}
+
+// The owner's claims from the front (q the pass's word).  A range that is
+// all this workgroup's has every slice taken (taken = issued = S) and q a
+// word of its own, which it reads after every tile like a claim, so that
+// one instance of each pass serves both.  Slice s starts at tile s tps; its claim is issued
+// when t = s tps - 1 tiles are done and checked one tile later, before the
+// slice's first tile is processed.  after_tile() is true when that slice is
+// a helper's: the stream stops there, with slices [0, taken) done.  Thread
+// 0 adds to the word after every tile (1 for a claim, else 0: a read), so
+// that its result is defined on every path and waited for only where it is
+// read.  go: two LDS words, used in turn (one barrier per check).
+// A pass with no claims (every instance that shares nothing, and a
+// helper's slice): the whole range is this workgroup's.
+struct NoClaims {
+    int taken;
+    int ntile = 0;
+    __device__ __forceinline__ bool after_tile(uint32_t*) { return false; }
+};
+struct FrontClaims {
+    uint32_t* q;
+    int S, tps, taken;
+    int issued;          // slices [0, issued) claimed or pre-owned (at first, taken)
+    int ntile = 0, t = 0;
+    uint32_t pend = 0;   // (thread 0) the word before the last addition
+    __device__ __forceinline__ bool after_tile(uint32_t* go)
+    {
+        ++t;
+        if (taken < issued && t == taken * tps && t < ntile) {
+            uint32_t* g = go + (taken & 1);
+            if (threadIdx.x == 0) *g = (pend & 0xFFFFu) + (pend >> 16) < (uint32_t)S ? 1u : 0u;
+            __syncthreads();
+            if (*g == 0u) return true;
+            ++taken;
+        }
+        const bool claim = issued < S && t == issued * tps - 1;
+        // (the address passes through a register, so the compiler does not
+        // aggregate the addition over the wave, which would wait for its
+        // result at once; a global pointer, since a flat access would also
+        // hold the LDS counter)
+        typedef __attribute__((address_space(1))) uint32_t gu32;
+        gu32* qv = (gu32*)q;
+        asm volatile("" : "+v"(qv));
+        uint32_t nv = 0u;
+        if (threadIdx.x == 0) nv = __hip_atomic_fetch_add(qv, claim ? 1u : 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        pend = nv;
+        issued += claim ? 1 : 0;
+        return false;
+    }
+};
+
+// ---- the two passes over a range [s0, s0 + n) of the row (a whole row, or
+// one slice; s0 a multiple of 32 so that the history bitmap's words align)
+
+// Pass 1: extremes (fmx, fmn), the elements at or above yhi into this
+// wave's segment (cw entries; *ovf set when it runs full), every other
+// element counted in its bin of CH.  fresh: rs already streams this range
+// (the row's first tiles, issued at the kernel's start).  fc: the owner's
+// claims of a shared row's slices (a workgroup's own range: all slices
+// taken, fc.q a word of its own, see FrontClaims).
+template <typename TIn, class FC>
+__device__ __forceinline__ void w2_pass1(RowStream<TIn>& rs, const TIn* rowp, int s0, int n, const uint32_t* bm,
+                                         bool pen_on, float pen,
+                                         bool neg, float yhi, float ylo, float scale, uint32_t* CH,
+                                         uint32_t* wck, uint32_t* wci, uint32_t& cw, float& fmx, float& fmn,
+                                         uint32_t* ovf, uint32_t* dummy, FC& fc, uint32_t* go,
+                                         bool fresh = false)
+{
+    const int lane = lane_id();
+    auto yv = [&](float x) { return neg ? -x : x; };
+    auto bin_of = [&](float y) -> uint32_t {   // (a NaN goes to bin 0)
+        const float f = (y - ylo) * scale;
+        return f >= 1.0f ? (f < 2047.0f ? (uint32_t)f : 2047u) : 0u;
+    };
+    float tx[FPT];
+    uint32_t nhit = 0;
+    if (!fresh) rs.retarget(rowp + s0, n);
+    fc.ntile = rs.ntile;
+    rs.run_pen_all(pen_on ? bm + (s0 >> 5) : bm, pen_on, pen,
+        [&](int i, int, float x, bool valid) {
+            fmx = __builtin_elementwise_maximum(fmx, x);
+            fmn = __builtin_elementwise_minimum(fmn, x);
+            const float y = yv(x);
+            const bool top = valid && y >= yhi;
+            tx[i] = top ? x : __builtin_nanf("");
+            nhit += top ? 1u : 0u;
+            atomicAdd(valid && !top ? &CH[bin_of(y)] : dummy, 1u);   // (no branch per element)
+        },
+        [&](auto&& id) -> bool {
+            const uint32_t incl = wave_prefix_u32(nhit);
+            const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+            if (__builtin_expect(cw + tot > W2_SEG_USE, 0)) {
+                if (lane == 0) __hip_atomic_store(ovf, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                cw = W2_SEG_USE;   // (the rest of the range still counts toward the extremes)
+                nhit = 0;
+                return fc.after_tile(go);   // (the claims stay in step with the tiles)
+            }
+            uint32_t o = cw + incl - nhit;
+            const uint32_t dmy = W2_SEG_USE + (uint32_t)lane;
+#pragma unroll
+            for (int i = 0; i < FPT; ++i) {
+                const bool h = tx[i] == tx[i];
+                const uint32_t a = h ? o : dmy;
+                wck[a] = f2u(tx[i]);
+                wci[a] = (uint32_t)(s0 + id(i));
+                o += h ? 1u : 0u;
+            }
+            nhit = 0;
+            cw += tot;
+            return fc.after_tile(go);
+        });
+}
+
+// Pass 2: the exact masses of the elements below yhi summed (wb), and those
+// at or above ycb (ac) and ydb (ad); the elements of the windows [yca, ycb)
+// and [yda, ydb) listed in KC and KD (counts in cnt[0], cnt[1]).  fc as
+// for pass 1.
+template <typename TIn, class FC>
+__device__ __forceinline__ void w2_pass2(RowStream<TIn>& rs, const TIn* rowp, int s0, int n, const uint32_t* bm,
+                                         bool pen_on, float pen,
+                                         bool neg, float T, float m, float yhi, float yca, float ycb, float yda,
+                                         float ydb, u64& wb, u64& ac, u64& ad, uint32_t* cnt, u64* KC, u64* KD,
+                                         FC& fc, uint32_t* go)
+{
+    auto yv = [&](float x) { return neg ? -x : x; };
+    auto has_pen = [&](int e) { return pen_on && ((bm[e >> 5] >> (e & 31)) & 1u); };
+    uint32_t mc = 0, md = 0;   // this tile's window elements, a bit per slot
+    rs.retarget(rowp + s0, n);
+    fc.ntile = rs.ntile;
+    rs.run_pen_val(pen_on ? bm + (s0 >> 5) : bm, pen_on, pen,
+        [&](int i, int, float x) {
+            const float y = yv(x);
+            const float l = x / T;
+            const u64 wgt = y >= yhi ? 0ull : count_mass(1u, l - m);
+            wb += wgt;
+            ac += y >= ycb ? wgt : 0ull;
+            ad += y >= ydb ? wgt : 0ull;
+            mc |= (y >= yca && !(y >= ycb) ? 1u : 0u) << i;
+            md |= (y >= yda && !(y >= ydb) ? 1u : 0u) << i;
+        },
+        [&](auto&& id, auto&& val) -> bool {
+            if (__ballot((mc | md) != 0u)) {
+#pragma unroll
+                for (int i = 0; i < FPT; ++i) {
+                    if (((mc | md) >> i) & 1u) {
+                        const int e = s0 + id(i);
+                        float x = val(i);
+                        if (has_pen(e)) x = penalize(x, pen);
+                        const u64 key = ((u64)vkey(x / T) << 32) | (u64)(0xFFFFFFFFu - (uint32_t)e);
+                        if ((mc >> i) & 1u) {
+                            const uint32_t s = atomicAdd(&cnt[0], 1u);
+                            if (s < (uint32_t)LCAP) KC[s] = key;
+                        }
+                        if ((md >> i) & 1u) {
+                            const uint32_t s = atomicAdd(&cnt[1], 1u);
+                            if (s < (uint32_t)LCAP) KD[s] = key;
+                        }
+                    }
+                }
+            }
+            mc = 0;
+            md = 0;
+            return fc.after_tile(go);
+        });
+}
+
+// A helper's claim from the back of a pass (thread 0): the slice, or -1
+// when every slice is taken.
+__device__ __forceinline__ int wj_claim_back(uint32_t* q, int S)
+{
+    const uint32_t old = atomicAdd(q, 1u << 16);
+    return (old & 0xFFFFu) + (old >> 16) < (uint32_t)S ? S - 1 - (int)(old >> 16) : -1;
+}
+// Counts this workgroup's slice done, after every wave's results are
+// acknowledged (they were written through, or added at device scope).
+__device__ __forceinline__ void wj_done(uint32_t* done)
+{
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) atomicAdd(done, 1u);
+}
+// The owner's wait until the helpers finished need slices of a pass
+// (thread 0 polls, bounded); then their results are acquired.  False: the
+// wait timed out.
+__device__ __forceinline__ bool wj_wait(const uint32_t* done, int need)
+{
+    __shared__ int s_ok;
+    if (threadIdx.x == 0) {
+        int ok = need <= 0 ? 1 : 0;
+        for (int it = 0; it < WJ_SPIN && !ok; ++it) {
+            if (ld_dev(done) >= (uint32_t)need) ok = 1;
+            else __builtin_amdgcn_s_sleep(2);
+        }
+        if (ok) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        s_ok = ok;
+    }
+    __syncthreads();
+    const bool ok = s_ok != 0;
+    __syncthreads();
+    return ok;
+}
+
+template <typename TIn, bool SH>
 __device__ __forceinline__ int finish_wide2(const Params& p, int r, RowStream<TIn>& rs, float T, bool neg,
                                             float top_p, float u, float pen, bool pen_on, const uint32_t* bm,
-                                            const float (&sx)[NSAMP / NT], int se0, unsigned char* smem,
-                                            uint32_t* CH, Reduced& rd, int64_t& tok, int32_t& st)
+                                            const float (&sx)[NSAMP / NT], int se0, int h0, int h1,
+                                            unsigned char* smem, uint32_t* CH, Reduced& rd, int64_t& tok, int32_t& st)
 {
     constexpr int NS = NSAMP / NT;
-    __shared__ uint32_t w2_seg[NWAVES], w2_ovf, w2_cnt[2], w2_dummy;
+    __shared__ uint32_t w2_seg[NWAVES], w2_ovf, w2_cnt[2], w2_dummy, w2_go[2];
     __shared__ uint32_t w2_r[4][NWAVES];
     __shared__ u64 w2_s[3][NWAVES];
+    __shared__ int w2_job;
     const int tid = threadIdx.x, lane = lane_id(), wv = wave_id();
     const int V = p.V;
+    const TIn* rowp = (const TIn*)p.logits + (size_t)r * (size_t)p.ld;
     uint32_t* ck = (uint32_t*)(smem + KF_CK);
     uint32_t* ci = (uint32_t*)(smem + KF_CI);
     u64* TL = (u64*)(smem + KF_MH);
@@ -1651,52 +1943,89 @@ __device__ __forceinline__ int finish_wide2(const Params& p, int r, RowStream<TI
     if (!(yhi > ylo) || !__builtin_isfinite(scale) || !__builtin_isfinite(dy) || !(dy > 1000.0f * umax))
         return -1;
 
+    // The row's job: other workgroups may take slices of both passes, when
+    // the batch has rows that do not share (helpers), the row's vectors are
+    // whole (slices start at tiles), and no probabilities are written (that
+    // third read stays here).  The slot: the row's rank among the batch's
+    // rows with top-k off (the first WJ_NJOB of them share); in a batch of
+    // more than NT rows, r mod WJ_NJOB, held by the first row of the call
+    // to take it (another row goes alone).
+    typedef VecIO<TIn> IO;
+    const int ntile = (V / IO::W + NT * (FPT / IO::W) - 1) / (NT * (FPT / IO::W));
+    const int tps = (ntile + WJ_S - 1) / WJ_S;
+    const int S = (ntile + tps - 1) / tps;
+    const int f0 = S < (tps == 1 ? 2 : 1) ? S : (tps == 1 ? 2 : 1);   // the owner's slices from the start
+    const bool share = p.wj && !p.out_probs && sizeof(TIn) == 4 && (((uintptr_t)rowp) & 15u) == 0 &&
+                       V % IO::W == 0 && (p.B > NT || wide_rows_counted() < (uint32_t)p.B);
+    if (SH && tid == 0) {
+        int j = -1;
+        if (share && p.B <= NT) {
+            const int rk = wide_rank(r);
+            j = rk < WJ_NJOB ? rk : -1;
+        } else if (share) {
+            WideJob* Jc = wj_job(p.wj, r % WJ_NJOB);
+            if (atomicExch(&Jc->own, p.epoch) != p.epoch) j = r % WJ_NJOB;
+        }
+        w2_job = j;
+    }
+    int job = -1;   // (constant in the instance that shares nothing)
+    if constexpr (SH) {
+        __syncthreads();
+        job = w2_job;
+    }
+    WideJob* J = job >= 0 ? wj_job(p.wj, job) : nullptr;
+    // the word a pass of this workgroup's own reads after every tile
+    uint32_t* own_word = wj_own_word(p, r);
+    auto close_job = [&]() {   // no more slices; helpers leave the job
+        if (job >= 0) {
+            __syncthreads();
+            if (tid == 0) put_dev64(&J->tag, wj_tag(p.epoch, S, 3u));
+            job = -1;
+        }
+    };
+
     // pass 1
     const int w = wv;
     uint32_t* wck = ck + w * FSEG;
     uint32_t* wci = ci + w * FSEG;
     uint32_t cw = 0;
-    constexpr uint32_t SEG_USE = FSEG - 64;
     float fmx = -INFINITY, fmn = INFINITY;
-    float tx[FPT];
-    uint32_t nhit = 0;
-    auto bin_of = [&](float y) -> uint32_t {   // (a NaN goes to bin 0)
-        const float f = (y - ylo) * scale;
-        return f >= 1.0f ? (f < 2047.0f ? (uint32_t)f : 2047u) : 0u;
-    };
-    rs.run_pen_all(bm, pen_on, pen,
-        [&](int i, int, float x, bool valid) {
-            fmx = __builtin_elementwise_maximum(fmx, x);
-            fmn = __builtin_elementwise_minimum(fmn, x);
-            const float y = yv(x);
-            const bool top = valid && y >= yhi;
-            tx[i] = top ? x : __builtin_nanf("");
-            nhit += top ? 1u : 0u;
-            atomicAdd(valid && !top ? &CH[bin_of(y)] : &w2_dummy, 1u);   // (no branch per element)
-        },
-        [&](auto&& id) -> bool {
-            const uint32_t incl = wave_prefix_u32(nhit);
-            const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
-            if (__builtin_expect(cw + tot > SEG_USE, 0)) {
-                if (lane == 0) __hip_atomic_store(&w2_ovf, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                cw = SEG_USE;   // (the rest of the row still counts toward the extremes)
-                nhit = 0;
-                return false;
-            }
-            uint32_t o = cw + incl - nhit;
-            const uint32_t dummy = SEG_USE + (uint32_t)lane;
-#pragma unroll
-            for (int i = 0; i < FPT; ++i) {
-                const bool h = tx[i] == tx[i];
-                const uint32_t a = h ? o : dummy;
-                wck[a] = f2u(tx[i]);
-                wci[a] = (uint32_t)id(i);
-                o += h ? 1u : 0u;
-            }
-            nhit = 0;
-            cw += tot;
-            return false;
-        });
+    if (job >= 0) {   // pass 1 opens: its parameters, then the tag
+        uint32_t* gb = wj_bins(J);
+        for (int b = tid; b < 2048; b += NT) put_dev32(gb + b, 0u);
+        if (tid == 0) {
+            put_dev32(&J->tps, (uint32_t)tps);
+            put_dev32(&J->q1, (uint32_t)f0); put_dev32(&J->done1, 0u);
+            put_dev32((uint32_t*)&J->r, (uint32_t)r);
+            put_dev32((uint32_t*)&J->h0, (uint32_t)h0); put_dev32((uint32_t*)&J->h1, (uint32_t)h1);
+            put_devf(&J->T, T); put_devf(&J->pen, pen); put_devf(&J->yhi, yhi); put_devf(&J->ylo, ylo);
+            put_devf(&J->scale, scale);
+            put_dev32(&J->neg, neg ? 1u : 0u); put_dev32(&J->pen_on, pen_on ? 1u : 0u);
+            put_dev32(&J->gmax, 0u); put_dev32(&J->gmin, 0xFFFFFFFFu);
+            put_dev32(&J->ntop, 0u); put_dev32(&J->ovf, 0u);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0) put_dev64(&J->tag, wj_tag(p.epoch, S, 1u));
+    }
+    if constexpr (!SH) {
+        NoClaims fc{S};
+        w2_pass1<TIn>(rs, rowp, 0, V, bm, pen_on, pen, neg, yhi, ylo, scale, CH, wck, wci, cw, fmx, fmn, &w2_ovf,
+                      &w2_dummy, fc, w2_go, true);
+    } else for (bool fresh = true;; fresh = false) {   // (a second round only after a wait that timed out)
+        FrontClaims fc = job >= 0 ? FrontClaims{&J->q1, S, tps, f0, f0} : FrontClaims{own_word, S, tps, S, S};
+        w2_pass1<TIn>(rs, rowp, 0, V, bm, pen_on, pen, neg, yhi, ylo, scale, CH, wck, wci, cw, fmx, fmn, &w2_ovf,
+                      &w2_dummy, fc, w2_go, fresh);
+        if (job < 0 || wj_wait(&J->done1, S - fc.taken)) break;
+        // (never expected: then the pass again, here, with the helpers' parts ignored)
+        close_job();
+        for (int b = tid; b < 2048; b += NT) CH[b] = 0;
+        if (tid == 0) w2_ovf = 0;
+        __syncthreads();
+        cw = 0;
+        fmx = -INFINITY;
+        fmn = INFINITY;
+    }
     uint32_t omax, omin;
     if (fmx != fmx) {   // a NaN (both extremes carry it): keys that say so
         omax = 0xFFFFFFFFu;
@@ -1719,21 +2048,43 @@ __device__ __forceinline__ int finish_wide2(const Params& p, int r, RowStream<TI
         off += v < w ? w2_seg[v] : 0u;
         ntop += w2_seg[v];
     }
+    // the helpers' part: extremes, bin counts, top-list entries
+    uint32_t gtop = 0;
+    bool govf = false;
+    if (job >= 0) {
+        const uint32_t gmx = ld_dev(&J->gmax), gmn = ld_dev(&J->gmin);
+        rd.max = gmx > rd.max ? gmx : rd.max;
+        rd.min = gmn < rd.min ? gmn : rd.min;
+        gtop = ld_dev(&J->ntop);
+        govf = ld_dev(&J->ovf) != 0u;
+        const uint32_t* gb = wj_bins(J);
+        for (int b = tid; b < 2048; b += NT) CH[b] += ld_dev(gb + b);
+    }
     // NaN keys lie above the key of +inf and below that of -inf
     const bool has_nan = rd.max > 0xFF800000u || rd.min < 0x007FFFFFu;
     const bool has_inf = rd.max >= 0xFF800000u || rd.min <= 0x007FFFFFu;
-    if (has_nan || (has_inf && __builtin_isinf(T))) { st = MXS_ROW_NONFINITE; tok = -1; return 1; }
+    if (has_nan || (has_inf && __builtin_isinf(T))) { close_job(); st = MXS_ROW_NONFINITE; tok = -1; return 1; }
     const float m = sel_inv(rd.max, neg) / T;
-    if (!isfinite(m)) { st = MXS_ROW_NONFINITE; tok = -1; return 1; }
-    if (top_p < 1.0f && !(top_p > 0.0f)) { st = MXS_ROW_EMPTY_NUCLEUS; tok = -1; return 1; }
-    if (w2_ovf || ntop > (uint32_t)TL_CAP) return 0;
+    if (!isfinite(m)) { close_job(); st = MXS_ROW_NONFINITE; tok = -1; return 1; }
+    if (top_p < 1.0f && !(top_p > 0.0f)) { close_job(); st = MXS_ROW_EMPTY_NUCLEUS; tok = -1; return 1; }
+    if (w2_ovf || govf || ntop + gtop > (uint32_t)TL_CAP) { close_job(); return 0; }
 
-    // the top list's keys and exact masses
+    // the top list's keys and exact masses (the helpers' entries after the owner's)
     u64 part = 0;
     for (uint32_t j = (uint32_t)lane; j < cw; j += 64) {
         const float l = u2f(wck[j]) / T;
         TL[off + j] = ((u64)vkey(l) << 32) | (u64)(0xFFFFFFFFu - wci[j]);
         part += mass_of(l - m);
+    }
+    if (job >= 0) {
+        const u64* gt = wj_top(J);
+        for (uint32_t j = (uint32_t)tid; j < gtop; j += NT) {
+            const u64 e = ld_dev64(gt + j);
+            const float l = u2f((uint32_t)(e >> 32)) / T;
+            TL[ntop + j] = ((u64)vkey(l) << 32) | (u64)(0xFFFFFFFFu - (uint32_t)e);
+            part += mass_of(l - m);
+        }
+        ntop += gtop;
     }
     const u64 Wtop = block_sum<u64>(part);   // (its barriers publish TL and the counts)
 
@@ -1830,44 +2181,30 @@ __device__ __forceinline__ int finish_wide2(const Params& p, int r, RowStream<TI
 
     // pass 2 (no branch per element: the rare window elements are marked,
     // and written at the tile's end by the waves that have any)
-    rs.restart();
     u64 wb = 0, ac = 0, ad = 0;
-    uint32_t mc = 0, md = 0;   // this tile's window elements, a bit per slot
-    rs.run_pen_val(bm, pen_on, pen,
-        [&](int i, int, float x) {
-            const float y = yv(x);
-            const float l = x / T;
-            const u64 wgt = y >= yhi ? 0ull : count_mass(1u, l - m);
-            wb += wgt;
-            ac += y >= ycb ? wgt : 0ull;
-            ad += y >= ydb ? wgt : 0ull;
-            mc |= (y >= yca && !(y >= ycb) ? 1u : 0u) << i;
-            md |= (y >= yda && !(y >= ydb) ? 1u : 0u) << i;
-        },
-        [&](auto&& id, auto&& val) -> bool {
-            if (__ballot((mc | md) != 0u)) {
-#pragma unroll
-                for (int i = 0; i < FPT; ++i) {
-                    if (((mc | md) >> i) & 1u) {
-                        const int e = id(i);
-                        float x = val(i);
-                        if (has_pen(e)) x = penalize(x, pen);
-                        const u64 key = ((u64)vkey(x / T) << 32) | (u64)(0xFFFFFFFFu - (uint32_t)e);
-                        if ((mc >> i) & 1u) {
-                            const uint32_t s = atomicAdd(&w2_cnt[0], 1u);
-                            if (s < (uint32_t)LCAP) KC[s] = key;
-                        }
-                        if ((md >> i) & 1u) {
-                            const uint32_t s = atomicAdd(&w2_cnt[1], 1u);
-                            if (s < (uint32_t)LCAP) KD[s] = key;
-                        }
-                    }
-                }
-            }
-            mc = 0;
-            md = 0;
-            return false;
-        });
+    if (job >= 0 && tid == 0) {   // pass 2 opens
+        put_dev32(&J->q2, (uint32_t)f0); put_dev32(&J->done2, 0u);
+        put_devf(&J->m, m); put_devf(&J->yca, yca); put_devf(&J->ycb, ycb);
+        put_devf(&J->yda, yda); put_devf(&J->ydb, ydb);
+        put_dev32(&J->nc, 0u); put_dev32(&J->nd, 0u);
+        put_dev64(&J->wb, 0ull); put_dev64(&J->ac, 0ull); put_dev64(&J->ad, 0ull);
+        __builtin_amdgcn_s_waitcnt(0);
+        put_dev64(&J->tag, wj_tag(p.epoch, S, 2u));
+    }
+    if constexpr (!SH) {
+        NoClaims fc{S};
+        w2_pass2<TIn>(rs, rowp, 0, V, bm, pen_on, pen, neg, T, m, yhi, yca, ycb, yda, ydb, wb, ac, ad, w2_cnt, KC, KD,
+                      fc, w2_go);
+    } else for (;;) {   // (as for pass 1)
+        FrontClaims fc = job >= 0 ? FrontClaims{&J->q2, S, tps, f0, f0} : FrontClaims{own_word, S, tps, S, S};
+        w2_pass2<TIn>(rs, rowp, 0, V, bm, pen_on, pen, neg, T, m, yhi, yca, ycb, yda, ydb, wb, ac, ad, w2_cnt, KC, KD,
+                      fc, w2_go);
+        if (job < 0 || wj_wait(&J->done2, S - fc.taken)) break;
+        close_job();
+        if (tid == 0) { w2_cnt[0] = 0; w2_cnt[1] = 0; }
+        __syncthreads();
+        wb = 0; ac = 0; ad = 0;
+    }
     {
         const u64 a0 = wave_sum_u64(wb), a1 = wave_sum_u64(ac), a2 = wave_sum_u64(ad);
         if (lane == 0) { w2_s[0][w] = a0; w2_s[1][w] = a1; w2_s[2][w] = a2; }
@@ -1876,7 +2213,21 @@ __device__ __forceinline__ int finish_wide2(const Params& p, int r, RowStream<TI
     u64 WB = 0, AC = 0, AD = 0;
 #pragma unroll
     for (int v = 0; v < NWAVES; ++v) { WB += w2_s[0][v]; AC += w2_s[1][v]; AD += w2_s[2][v]; }
-    const uint32_t nc = w2_cnt[0], nd = w2_cnt[1];
+    uint32_t nc = w2_cnt[0], nd = w2_cnt[1];
+    if (job >= 0) {   // the helpers' sums and window elements
+        WB += ld_dev64(&J->wb);
+        AC += ld_dev64(&J->ac);
+        AD += ld_dev64(&J->ad);
+        const uint32_t gc = ld_dev(&J->nc), gd = ld_dev(&J->nd);
+        if (nc + gc <= (uint32_t)LCAP && nd + gd <= (uint32_t)LCAP) {
+            const u64 *gkc = wj_kc(J), *gkd = wj_kd(J);
+            for (uint32_t j = (uint32_t)tid; j < gc; j += NT) KC[nc + j] = ld_dev64(gkc + j);
+            for (uint32_t j = (uint32_t)tid; j < gd; j += NT) KD[nd + j] = ld_dev64(gkd + j);
+        }
+        nc += gc;
+        nd += gd;
+        close_job();   // (its barrier publishes the lists)
+    }
     const u64 W = Wtop + WB;
     if (W < Wlo || W > Whi || nc > (uint32_t)LCAP || nd > (uint32_t)LCAP) return 0;
 
@@ -1923,6 +2274,203 @@ __device__ __forceinline__ int finish_wide2(const Params& p, int r, RowStream<TI
             [&](auto&&) { return false; });
     }
     return 1;
+}
+
+// A workgroup that has finished its own row takes slices of the shared
+// rows' open passes from the back until none is left and no job is pending;
+// while jobs are pending but no slice is open it waits (bounded; only when
+// every row's workgroup was resident from the start, p.help).  Nothing is
+// polled when the batch has no row with top-k off, or has only such rows
+// (then no row shares).  Wave 0 reads every job's tag and claims at once
+// (a lane per job); a helper stays with its job while it has slices (its
+// next claim rides with the flush of the last slice).  Its LDS is free: the
+// history bitmap of a job's row is rebuilt here, and each slice's bins,
+// top-list entries and window elements are counted here first, then added
+// to the job's records.
+template <typename TIn>
+__device__ __forceinline__ void help_rows(const Params& p, unsigned char* smem)
+{
+    if constexpr (sizeof(TIn) != 4) {
+        return;
+    } else {
+        __shared__ int hc_job, hc_phase, hc_slice, hc_S;
+        __shared__ uint32_t hc_ovf, hc_dummy, hc_cnt[2], hc_base[2], hc_go[2];
+        if (p.B <= NT) {
+            const uint32_t nw = wide_rows_counted();
+            if (nw == 0u || nw >= (uint32_t)p.B) return;
+        }
+        const int tid = threadIdx.x, lane = lane_id(), w = wave_id();
+        const int V = p.V;
+        uint32_t* bm = (uint32_t*)(smem + KF_BM);
+        uint32_t* CH = (uint32_t*)(smem + KF_H);
+        uint32_t* ck = (uint32_t*)(smem + KF_CK);
+        uint32_t* ci = (uint32_t*)(smem + KF_CI);
+        u64* KC = (u64*)(smem + W2_KC);
+        u64* KD = (u64*)(smem + W2_KD);
+        int built = -1;   // the job whose row's history bitmap is in bm
+        RowStream<TIn> rs((const TIn*)p.logits, 0, false);
+        int j = -1, phase = 0, s = -1, S = 0;   // the slice in hand (s >= 0)
+        for (int idle = 0; idle < WJ_SPIN;) {
+            if (s < 0) {
+                if (w == 0) {
+                    // lane l: job l's tag and claims
+                    u64 tg = 0, qq = 0;
+                    if (lane < WJ_NJOB) {
+                        WideJob* Jl = wj_job(p.wj, lane);
+                        tg = ld_dev64(&Jl->tag);
+                        qq = ld_dev64((const u64*)&Jl->q1);
+                    }
+                    const uint32_t ph = (uint32_t)tg & 0xFFu, Sl = (uint32_t)(tg >> 8) & 0xFFu;
+                    const bool live = lane < WJ_NJOB && (uint32_t)(tg >> 32) == p.epoch &&
+                                      ((uint32_t)(tg >> 16) & 0xFFFFu) == WJ_MAGIC && (ph == 1u || ph == 2u);
+                    const uint32_t q = ph == 1u ? (uint32_t)qq : (uint32_t)(qq >> 32);
+                    const bool open = live && (q & 0xFFFFu) + (q >> 16) < Sl;
+                    const u64 om = __ballot(open), lm = __ballot(live);
+                    int cmd = -2, cph = 0, cs = -1, cS = 0;
+                    if (om) {
+                        // this workgroup's last job first, then the others from blockIdx mod WJ_NJOB
+                        int pick = (j >= 0 && ((om >> j) & 1u)) ? j : -1;
+                        for (int i = 0; i < WJ_NJOB && pick < 0; ++i) {
+                            const int l = ((int)blockIdx.x + i) % WJ_NJOB;
+                            if ((om >> l) & 1u) pick = l;
+                        }
+                        cph = __builtin_amdgcn_readlane((int)ph, pick);
+                        cS = __builtin_amdgcn_readlane((int)Sl, pick);
+                        if (lane == 0) {
+                            WideJob* Jp = wj_job(p.wj, pick);
+                            cs = wj_claim_back(cph == 1 ? &Jp->q1 : &Jp->q2, cS);
+                        }
+                        cmd = pick;   // (a refused claim: scan again at once)
+                    } else if (lm && p.help) {
+                        cmd = -1;     // jobs pending: wait
+                    }
+                    if (lane == 0) { hc_job = cmd; hc_phase = cph; hc_slice = cs; hc_S = cS; }
+                }
+                __syncthreads();
+                const int cmd = hc_job;
+                s = hc_slice;
+                __syncthreads();
+                if (cmd == -2) break;
+                if (cmd == -1 || s < 0) {
+                    if (cmd == -1) __builtin_amdgcn_s_sleep(8);   // (about 200 ns between polls)
+                    ++idle;
+                    s = -1;
+                    continue;
+                }
+                j = cmd;
+                phase = hc_phase;
+                S = hc_S;
+            }
+            idle = 0;
+            WideJob* J = wj_job(p.wj, j);
+            // the job's parameters (read at device scope: the owner wrote them through)
+            const int r = (int)ld_dev((const uint32_t*)&J->r), tps = (int)ld_dev(&J->tps);
+            const bool neg = ld_dev(&J->neg) != 0u, pen_on = ld_dev(&J->pen_on) != 0u;
+            const float T = ld_devf(&J->T), pen = ld_devf(&J->pen), yhi = ld_devf(&J->yhi);
+            if ((unsigned)r >= (unsigned)p.B || tps < 1) {   // (not a record of this call: leave it)
+                s = -1;
+                j = -1;
+                continue;
+            }
+            const TIn* rowp = (const TIn*)p.logits + (size_t)r * (size_t)p.ld;
+            const int L = tps * FTILE;
+            const int s0 = s * L < V ? s * L : V;
+            const int n = (s0 + L < V ? s0 + L : V) - s0;
+            if (pen_on && built != j) {   // the row's history (its ids were checked by the owner)
+                const int h0 = (int)ld_dev((const uint32_t*)&J->h0), h1 = (int)ld_dev((const uint32_t*)&J->h1);
+                const int words = (V + 31) >> 5;
+                for (int wd = tid; wd < words; wd += NT) bm[wd] = 0;
+                __syncthreads();
+                for (int h = h0 + tid; h < h1; h += NT) {
+                    const int id = p.hids[h];
+                    if (id >= 0 && id < V) atomicOr(&bm[id >> 5], 1u << (id & 31));
+                }
+                __syncthreads();
+                built = j;
+            }
+            NoClaims mine{S};
+            uint32_t* q;
+            uint32_t* done;
+            if (phase == 1) {
+                const float ylo = ld_devf(&J->ylo), scale = ld_devf(&J->scale);
+                for (int b = tid; b < 2048; b += NT) CH[b] = 0;
+                if (tid == 0) hc_ovf = 0;
+                __syncthreads();
+                uint32_t cw = 0;
+                float fmx = -INFINITY, fmn = INFINITY;
+                w2_pass1<TIn>(rs, rowp, s0, n, bm, pen_on, pen, neg, yhi, ylo, scale, CH, ck + w * FSEG,
+                              ci + w * FSEG, cw, fmx, fmn, &hc_ovf, &hc_dummy, mine, hc_go);
+                uint32_t omax, omin;
+                if (fmx != fmx) {
+                    omax = 0xFFFFFFFFu;
+                    omin = 0u;
+                } else {
+                    omax = neg ? selkey(fmn, true) : selkey(fmx, false);
+                    omin = neg ? selkey(fmx, true) : selkey(fmn, false);
+                }
+                const Reduced rw = block_reduce(omax, omin, 0u);   // (its barriers publish CH and the segments)
+                uint32_t* gb = wj_bins(J);
+                for (int b = tid; b < 2048; b += NT) {
+                    const uint32_t c = CH[b];
+                    if (c) atomicAdd(gb + b, c);
+                }
+                // this wave's top-list entries after the others' (one atomic per wave)
+                uint32_t base = 0;
+                if (lane == 0 && cw) base = atomicAdd(&J->ntop, cw);
+                base = (uint32_t)__builtin_amdgcn_readlane((int)base, 0);
+                u64* gt = wj_top(J);
+                const uint32_t* wck = ck + w * FSEG;
+                const uint32_t* wci = ci + w * FSEG;
+                for (uint32_t i = (uint32_t)lane; i < cw; i += 64)
+                    if (base + i < (uint32_t)WJ_TOP) put_dev64(gt + base + i, ((u64)wck[i] << 32) | wci[i]);
+                if (tid == 0) {
+                    atomicMax(&J->gmax, rw.max);
+                    atomicMin(&J->gmin, rw.min);
+                    if (hc_ovf) put_dev32(&J->ovf, 1u);
+                }
+                if (lane == 0 && base + cw > (uint32_t)WJ_TOP) put_dev32(&J->ovf, 1u);
+                q = &J->q1;
+                done = &J->done1;
+            } else {
+                const float m = ld_devf(&J->m), yca = ld_devf(&J->yca), ycb = ld_devf(&J->ycb);
+                const float yda = ld_devf(&J->yda), ydb = ld_devf(&J->ydb);
+                if (tid == 0) { hc_cnt[0] = 0; hc_cnt[1] = 0; }
+                __syncthreads();
+                u64 wb = 0, ac = 0, ad = 0;
+                w2_pass2<TIn>(rs, rowp, s0, n, bm, pen_on, pen, neg, T, m, yhi, yca, ycb, yda, ydb, wb, ac, ad, hc_cnt,
+                              KC, KD, mine, hc_go);
+                const u64 a0 = wave_sum_u64(wb), a1 = wave_sum_u64(ac), a2 = wave_sum_u64(ad);
+                if (lane == 0) {
+                    atomicAdd(&J->wb, a0);
+                    atomicAdd(&J->ac, a1);
+                    atomicAdd(&J->ad, a2);
+                }
+                __syncthreads();   // (the lists are complete)
+                const uint32_t nc = hc_cnt[0] < (uint32_t)LCAP ? hc_cnt[0] : (uint32_t)LCAP;
+                const uint32_t nd = hc_cnt[1] < (uint32_t)LCAP ? hc_cnt[1] : (uint32_t)LCAP;
+                if (tid == 0) {
+                    // (a count past LCAP makes the owner's total exceed it: the owner then takes the general path)
+                    hc_base[0] = hc_cnt[0] ? atomicAdd(&J->nc, hc_cnt[0]) : 0u;
+                    hc_base[1] = hc_cnt[1] ? atomicAdd(&J->nd, hc_cnt[1]) : 0u;
+                }
+                __syncthreads();
+                const uint32_t bc = hc_base[0], bd = hc_base[1];
+                u64 *gkc = wj_kc(J), *gkd = wj_kd(J);
+                for (uint32_t i = (uint32_t)tid; i < nc; i += NT)
+                    if (bc + i < (uint32_t)WJ_WIN) put_dev64(gkc + bc + i, KC[i]);
+                for (uint32_t i = (uint32_t)tid; i < nd; i += NT)
+                    if (bd + i < (uint32_t)WJ_WIN) put_dev64(gkd + bd + i, KD[i]);
+                q = &J->q2;
+                done = &J->done2;
+            }
+            // the next slice of this pass, claimed while the results are acknowledged
+            if (tid == 0) hc_slice = wj_claim_back(q, S);
+            wj_done(done);
+            __syncthreads();
+            s = hc_slice;
+            __syncthreads();
+        }
+    }
 }
 
 // ---------------------------------------------------------------- fp16 rows, top-k off
@@ -2671,6 +3219,9 @@ __device__ __forceinline__ void fused_row(const Params p, const int r, unsigned 
     __shared__ uint32_t s_nh;                   // distinct history ids listed in hl
     __shared__ u64 s_ms[64];                    // masses per group of 32 bins
     __shared__ uint32_t s_cs[64];               // counts per group of 32 bins
+    __shared__ u64 s_rp[NWAVES], s_hp[NWAVES];  // raw_extremes: per-wave results
+    __shared__ uint32_t s_mn[NWAVES];
+    __shared__ uint32_t s_r[5][NWAVES];         // per-wave reductions after the stream
 
     const int tid = threadIdx.x, lane = lane_id();
     const int V = p.V;
@@ -2692,6 +3243,15 @@ __device__ __forceinline__ void fused_row(const Params p, const int r, unsigned 
     pa = (lane == 5 && p.hoff) ? (const uint32_t*)(p.hend ? p.hend + r : p.hoff + r + 1) : pa;
     pa = (lane == 6 && p.U) ? (const uint32_t*)(p.U + r) : pa;
     const uint32_t pv = *pa;
+    // k_fused: the batch's rows with top-k off (whether rows are shared),
+    // among the first NT rows, each wave counting 64; read with the parameters
+    int kb = 0;
+    float tb = 0.0f;
+    if constexpr (!SPLIT) {
+        const int i = tid < p.B ? tid : 0;
+        kb = p.K[i];
+        tb = p.T[i];
+    }
     // the slice headers of this row (a slice count per lane)
     uint32_t sln = 0;
     if constexpr (SPLIT) sln = p.sl_hdr[(size_t)(r * p.G + (lane < p.G ? lane : 0)) * SL_HDR];
@@ -2721,6 +3281,12 @@ __device__ __forceinline__ void fused_row(const Params p, const int r, unsigned 
     const int hv0 = __builtin_amdgcn_readlane((int)pv, 4);
     const int hv1 = __builtin_amdgcn_readlane((int)pv, 5);
     const float uv = __builtin_bit_cast(float, (uint32_t)__builtin_amdgcn_readlane((int)pv, 6));
+    if constexpr (!SPLIT) {
+        const bool wd = sizeof(TIn) == 4 && tid < p.B && tb != 0.0f && tb == tb && (kb <= 0 || kb >= V) &&
+                        V >= FAST_MIN_V;
+        const u64 wm = __ballot(wd);
+        if (lane == 0) g_wide[wave_id()] = wm;
+    }
     int h0, h1;
     bool hbad;
     history_range(p, hv0, hv1, pen, h0, h1, hbad);
@@ -2846,8 +3412,6 @@ __device__ __forceinline__ void fused_row(const Params p, const int r, unsigned 
     const bool raw_ok = pen_on && pen > 0.0f && pen <= 3.402823466e38f &&
                         (mode == MODE_GREEDY || mode == MODE_LARGE);
     auto raw_extremes = [&](auto key_of, u64& best, uint32_t& kmin) -> bool {
-        __shared__ u64 s_rp[NWAVES], s_hp[NWAVES];
-        __shared__ uint32_t s_mn[NWAVES];
         uint32_t bk = 0, bi = 0, mn = 0xFFFFFFFFu;
         rs.template run<false>(bm, pen,
             [&](int, int e, float x) {
@@ -2965,7 +3529,6 @@ __device__ __forceinline__ void fused_row(const Params p, const int r, unsigned 
         float m0 = 0.0f, lest = 0.0f;
         Reduced rd{0u, 0xFFFFFFFFu, 0u};
         u64* MH = (u64*)(smem + KF_MH);
-        __shared__ uint32_t s_r[5][NWAVES];
         if (mode == MODE_TOPK) {
             // 1. A conservative estimate of the k-th largest key from a strided
             //    sample of NSAMP logits: the lower edge of the histogram bin
@@ -3318,7 +3881,7 @@ __device__ __forceinline__ void fused_row(const Params p, const int r, unsigned 
                 if (!overflow) fix_up();
             }
         } else if (mode == MODE_LARGE && (k <= 0 || k >= V) && V >= FAST_MIN_V &&
-                   (wide2 = finish_wide2<TIn>(p, r, rs, T, neg, top_p, u, pen, pen_on, bm, sx, se0, smem, hist,
+                   (wide2 = finish_wide2<TIn, !SPLIT>(p, r, rs, T, neg, top_p, u, pen, pen_on, bm, sx, se0, h0, h1, smem, hist,
                                               rd, tok, st)) >= 0) {
             // top-k off, two passes (done, or rd holds the extremes for the general path)
             have_rd = true;
@@ -3444,12 +4007,17 @@ __device__ __forceinline__ void fused_row(const Params p, const int r, unsigned 
     }
 }
 
-// Batches above SPLIT_MAX_B rows: one workgroup per row.
+// Batches above SPLIT_MAX_B rows: one workgroup per row; then it helps
+// with the top-k-off rows still running (help_rows).
 template <typename TIn>
 __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
 {
     extern __shared__ __align__(16) unsigned char smem[];
     fused_row<TIn, false>(p, (int)blockIdx.x, smem);
+    if (p.wj) {
+        __syncthreads();   // (the row's LDS is free)
+        help_rows<TIn>(p, smem);
+    }
 }
 
 // Batches of up to SPLIT_MAX_B rows, in one launch: workgroup (g, r) runs

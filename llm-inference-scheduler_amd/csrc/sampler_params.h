@@ -36,6 +36,15 @@ struct Params {
     // the rows' packed maxima from the LM head's epilogue (NULL: none):
     // (greedy key << 32) | ~index, the token of a greedy row without a penalty
     const unsigned long long* pre_best;
+    // top-k-off rows shared with helpers (k_fused; NULL: none): the job
+    // records, this call's epoch (tags them), and whether every row's
+    // workgroup is resident from the start (helpers may wait)
+    unsigned char* wj;
+    unsigned int epoch;
+    int help;
+    // (every launch) lines of the workspace whose words the passes of
+    // finish_wide2 read when no row is shared (WJ_OWN lines of 64 bytes)
+    unsigned int* wown;
 };
 
 // ---------------------------------------------------------------- small batches
@@ -56,6 +65,27 @@ constexpr size_t SL_WS_BYTES = SL_HDR_BYTES + (size_t)SPLIT_SLICES * SLICE_CAP *
 __host__ __device__ __forceinline__ int split_slices(int B) { return B <= 4 ? 64 : SPLIT_SLICES / B; }
 static_assert(SPLIT_MAX_B * (SPLIT_SLICES / SPLIT_MAX_B) <= SPLIT_SLICES && 4 * 64 <= SPLIT_SLICES &&
               SPLIT_SLICES / 5 <= 64, "B * G <= SPLIT_SLICES and G <= 64 (one header per lane)");
+
+// ---------------------------------------------------------------- rows shared with helpers
+//
+// In k_fused (more than SPLIT_MAX_B rows), a row with top-k off reads its
+// logits twice (finish_wide2), about four times as long as a top-k row.  Its
+// workgroup (the owner) opens each pass as at most WJ_S slices of whole
+// tiles; workgroups that have finished their own rows take slices from the
+// back while the owner streams from the front, and hand their results over
+// through the workspace, the owner merges them with its own.  The records:
+// WJ_NJOB jobs (row r uses job r mod WJ_NJOB), each a header of WJ_HDR
+// bytes, the helpers' bin counts (2048 u32), top-list entries (WJ_TOP u64)
+// and window elements (2 x WJ_WIN u64).  Every record carries the call's
+// epoch, so a call needs no reset of the previous call's state.
+constexpr int WJ_NJOB = 16;
+constexpr int WJ_S = 32;
+constexpr int WJ_TOP = 2048;
+constexpr int WJ_WIN = 4096;
+constexpr size_t WJ_HDR = 256;
+constexpr size_t WJ_JOB_BYTES = WJ_HDR + 4 * 2048 + 8 * (size_t)WJ_TOP + 2 * 8 * (size_t)WJ_WIN;
+constexpr int WJ_OWN = 512;   // then a 64-byte line per row (rows r mod WJ_OWN), Params::wown
+constexpr size_t WJ_BYTES = WJ_NJOB * WJ_JOB_BYTES + 64 * (size_t)WJ_OWN;
 
 // The launchers of the kernel instances (k_f32.hip, k_f16.hip,
 // k_f32_split.hip, k_f16_split.hip).  Each returns the first HIP error of
