@@ -68,7 +68,7 @@ const char* mxs_status_string(int status);
 
 /*
  * Workspace size in bytes for a batch of B rows of V logits (the same for
- * every valid shape, about 4.3 MiB): batches of up to 64 rows split each row
+ * every valid shape, about 4.8 MiB): batches of up to 64 rows split each row
  * across several workgroups, which hand their candidates over in the
  * workspace and count themselves done on a per-row counter kept there;
  * larger batches keep every row's state on chip, and a row with top-k off
@@ -191,7 +191,7 @@ int mxs_sample_head(const void* logits, int dtype, int B, int V, int64_t ld,
  * GPU (different streams, or different threads) race and must be
  * serialized by the caller.  Arguments and results are as for mxs_sample.
  */
-#define MXS_NOALLOC_SCRATCH_BYTES 4501504
+#define MXS_NOALLOC_SCRATCH_BYTES 5044224
 int mxs_sample_noalloc(const void* logits, int dtype, int B, int V, int64_t ld,
                        const float* temperature, const int32_t* top_k,
                        const float* top_p, const float* penalty,

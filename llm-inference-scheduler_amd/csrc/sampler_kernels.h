@@ -1616,7 +1616,7 @@ constexpr int W2_KD = KF_CK + 8 * LCAP;  //         the draw's window (LCAP u64)
 constexpr int W2_SMH = KF_CK + 16 * LCAP;   // pick_in_set's masses (2048 u64)
 static_assert(W2_SMH + 16384 <= KF_HL, "the windows and pick_in_set's masses fit below the history list");
 static_assert(TL_CAP * 8 <= KF_H - KF_MH, "the top list fits where the mass histogram was");
-static_assert(WJ_TOP == TL_CAP && WJ_WIN == LCAP, "a job's lists hold what the owner's do");
+static_assert(WJ_S * WJ_TOPS == TL_CAP && WJ_S * WJ_WINS == LCAP, "a job's lists hold what the owner's do");
 constexpr uint32_t W2_SEG_USE = FSEG - 64;   // a wave segment's room (the rest: dummy slots)
 
 // ---- shared rows: the records (sampler_params.h has their layout)
@@ -1639,9 +1639,7 @@ struct WideJob {
     float T, pen, yhi, ylo, scale, m, yca, ycb, yda, ydb;
     uint32_t neg, pen_on;
     uint32_t gmax, gmin;              // pass 1: the helpers' key extremes
-    uint32_t ntop, ovf;               // pass 1: their top-list entries; a list or segment ran full
-    uint32_t nc, nd;                  // pass 2: their window elements
-    u64 wb, ac, ad;                   // pass 2: their sums
+    uint32_t ovf, pad1;               // pass 1: a helper's segment ran full
 };
 static_assert(sizeof(WideJob) <= WJ_HDR, "a job's header");
 static_assert(WJ_S < 256 && WJ_NJOB <= 64, "S fits the tag; one lane per job");
@@ -1653,9 +1651,15 @@ __device__ __forceinline__ WideJob* wj_job(unsigned char* wj, int j) { return (W
 // line each; beyond WJ_OWN they share)
 __device__ __forceinline__ uint32_t* wj_own_word(const Params& p, int r) { return p.wown + (size_t)(r % WJ_OWN) * 16; }
 __device__ __forceinline__ uint32_t* wj_bins(WideJob* J) { return (uint32_t*)((unsigned char*)J + WJ_HDR); }
-__device__ __forceinline__ u64* wj_top(WideJob* J) { return (u64*)(wj_bins(J) + 2048); }
-__device__ __forceinline__ u64* wj_kc(WideJob* J) { return wj_top(J) + WJ_TOP; }
-__device__ __forceinline__ u64* wj_kd(WideJob* J) { return wj_kc(J) + WJ_WIN; }
+// slice s's top-list entries and window elements, the slices' counts of
+// them ([0]: top list, [1], [2]: windows, WJ_S each), the history bitmap
+__device__ __forceinline__ u64* wj_top(WideJob* J, int s) { return (u64*)(wj_bins(J) + 2048) + (size_t)s * WJ_TOPS; }
+__device__ __forceinline__ u64* wj_kc(WideJob* J, int s) { return wj_top(J, WJ_S) + (size_t)s * WJ_WINS; }
+__device__ __forceinline__ u64* wj_kd(WideJob* J, int s) { return wj_kc(J, WJ_S) + (size_t)s * WJ_WINS; }
+__device__ __forceinline__ uint32_t* wj_cnt(WideJob* J, int list) { return (uint32_t*)wj_kd(J, WJ_S) + list * WJ_S; }
+__device__ __forceinline__ uint32_t* wj_bm(WideJob* J) { return wj_cnt(J, 3); }
+// slice s's pass-2 sums: wb, ac, ad at [0], [WJ_S], [2 WJ_S]
+__device__ __forceinline__ u64* wj_sums(WideJob* J, int s) { return (u64*)(wj_bm(J) + WJ_BMW) + s; }
 __device__ __forceinline__ u64 wj_tag(uint32_t epoch, int S, uint32_t phase)
 {
     return ((u64)epoch << 32) | ((u64)WJ_MAGIC << 16) | ((u64)S << 8) | phase;
@@ -1709,7 +1713,9 @@ __device__ __forceinline__ int wide_rank(int r)
 // that its result is defined on every path and waited for only where it is
 // read.  go: two LDS words, used in turn (one barrier per check).
 // A pass with no claims (every instance that shares nothing, and a
-// helper's slice): the whole range is this workgroup's.
+// helper's slice): the whole range is this workgroup's.  (Its go words
+// are never touched.)
+__device__ __forceinline__ uint32_t* hc_go_dummy() { return nullptr; }
 struct NoClaims {
     int taken;
     int ntile = 0;
@@ -1906,6 +1912,8 @@ __device__ __forceinline__ int finish_wide2(const Params& p, int r, RowStream<TI
 {
     constexpr int NS = NSAMP / NT;
     __shared__ uint32_t w2_seg[NWAVES], w2_ovf, w2_cnt[2], w2_dummy, w2_go[2];
+    __shared__ uint32_t w2_sc[WJ_S], w2_so[WJ_S], w2_tot;   // helpers' slices: counts, offsets, total
+    __shared__ u64 w2_hs[3];                                 // their pass-2 sums
     __shared__ uint32_t w2_r[4][NWAVES];
     __shared__ u64 w2_s[3][NWAVES];
     __shared__ int w2_job;
@@ -2002,12 +2010,17 @@ __device__ __forceinline__ int finish_wide2(const Params& p, int r, RowStream<TI
             put_devf(&J->scale, scale);
             put_dev32(&J->neg, neg ? 1u : 0u); put_dev32(&J->pen_on, pen_on ? 1u : 0u);
             put_dev32(&J->gmax, 0u); put_dev32(&J->gmin, 0xFFFFFFFFu);
-            put_dev32(&J->ntop, 0u); put_dev32(&J->ovf, 0u);
+            put_dev32(&J->ovf, 0u);
+        }
+        if (pen_on) {   // the history bitmap, which helpers read instead of the row's history
+            uint32_t* gm = wj_bm(J);
+            for (int wd = tid; wd < ((V + 31) >> 5); wd += NT) put_dev32(gm + wd, bm[wd]);
         }
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         if (tid == 0) put_dev64(&J->tag, wj_tag(p.epoch, S, 1u));
     }
+    int taken1 = S, taken2 = S;   // the owner's slices of each pass ([taken, S) the helpers')
     if constexpr (!SH) {
         NoClaims fc{S};
         w2_pass1<TIn>(rs, rowp, 0, V, bm, pen_on, pen, neg, yhi, ylo, scale, CH, wck, wci, cw, fmx, fmn, &w2_ovf,
@@ -2016,6 +2029,7 @@ __device__ __forceinline__ int finish_wide2(const Params& p, int r, RowStream<TI
         FrontClaims fc = job >= 0 ? FrontClaims{&J->q1, S, tps, f0, f0} : FrontClaims{own_word, S, tps, S, S};
         w2_pass1<TIn>(rs, rowp, 0, V, bm, pen_on, pen, neg, yhi, ylo, scale, CH, wck, wci, cw, fmx, fmn, &w2_ovf,
                       &w2_dummy, fc, w2_go, fresh);
+        taken1 = fc.taken;
         if (job < 0 || wj_wait(&J->done1, S - fc.taken)) break;
         // (never expected: then the pass again, here, with the helpers' parts ignored)
         close_job();
@@ -2048,6 +2062,21 @@ __device__ __forceinline__ int finish_wide2(const Params& p, int r, RowStream<TI
         off += v < w ? w2_seg[v] : 0u;
         ntop += w2_seg[v];
     }
+    // The helpers' slices [taken, S) of a list (0: top list, 1, 2: windows):
+    // their counts and offsets in w2_sc, w2_so, the total in w2_tot (wave
+    // 0, a lane per slice); a count above the slice's room is an overflow.
+    auto slice_counts = [&](int list, int taken, uint32_t room) -> bool {
+        if (w == 0) {
+            const uint32_t c = lane < S && lane >= taken ? ld_dev(wj_cnt(J, list) + lane) : 0u;
+            const uint32_t incl = wave_prefix_u32(c);
+            if (lane < WJ_S) { w2_sc[lane] = c; w2_so[lane] = incl - c; }
+            const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+            const bool big = __ballot(c > room) != 0;
+            if (lane == 0) w2_tot = big ? 0xFFFFFFFFu : tot;
+        }
+        __syncthreads();
+        return w2_tot != 0xFFFFFFFFu;
+    };
     // the helpers' part: extremes, bin counts, top-list entries
     uint32_t gtop = 0;
     bool govf = false;
@@ -2055,10 +2084,11 @@ __device__ __forceinline__ int finish_wide2(const Params& p, int r, RowStream<TI
         const uint32_t gmx = ld_dev(&J->gmax), gmn = ld_dev(&J->gmin);
         rd.max = gmx > rd.max ? gmx : rd.max;
         rd.min = gmn < rd.min ? gmn : rd.min;
-        gtop = ld_dev(&J->ntop);
         govf = ld_dev(&J->ovf) != 0u;
         const uint32_t* gb = wj_bins(J);
         for (int b = tid; b < 2048; b += NT) CH[b] += ld_dev(gb + b);
+        govf = !slice_counts(0, taken1, (uint32_t)WJ_TOPS) || govf;
+        gtop = govf ? 0u : w2_tot;
     }
     // NaN keys lie above the key of +inf and below that of -inf
     const bool has_nan = rd.max > 0xFF800000u || rd.min < 0x007FFFFFu;
@@ -2077,12 +2107,14 @@ __device__ __forceinline__ int finish_wide2(const Params& p, int r, RowStream<TI
         part += mass_of(l - m);
     }
     if (job >= 0) {
-        const u64* gt = wj_top(J);
-        for (uint32_t j = (uint32_t)tid; j < gtop; j += NT) {
-            const u64 e = ld_dev64(gt + j);
-            const float l = u2f((uint32_t)(e >> 32)) / T;
-            TL[ntop + j] = ((u64)vkey(l) << 32) | (u64)(0xFFFFFFFFu - (uint32_t)e);
-            part += mass_of(l - m);
+        for (int j = taken1 * WJ_TOPS + tid; j < S * WJ_TOPS; j += NT) {
+            const int sl = j / WJ_TOPS, i = j % WJ_TOPS;
+            if ((uint32_t)i < w2_sc[sl]) {
+                const u64 e = ld_dev64(wj_top(J, sl) + i);
+                const float l = u2f((uint32_t)(e >> 32)) / T;
+                TL[ntop + w2_so[sl] + i] = ((u64)vkey(l) << 32) | (u64)(0xFFFFFFFFu - (uint32_t)e);
+                part += mass_of(l - m);
+            }
         }
         ntop += gtop;
     }
@@ -2186,8 +2218,6 @@ __device__ __forceinline__ int finish_wide2(const Params& p, int r, RowStream<TI
         put_dev32(&J->q2, (uint32_t)f0); put_dev32(&J->done2, 0u);
         put_devf(&J->m, m); put_devf(&J->yca, yca); put_devf(&J->ycb, ycb);
         put_devf(&J->yda, yda); put_devf(&J->ydb, ydb);
-        put_dev32(&J->nc, 0u); put_dev32(&J->nd, 0u);
-        put_dev64(&J->wb, 0ull); put_dev64(&J->ac, 0ull); put_dev64(&J->ad, 0ull);
         __builtin_amdgcn_s_waitcnt(0);
         put_dev64(&J->tag, wj_tag(p.epoch, S, 2u));
     }
@@ -2199,6 +2229,7 @@ __device__ __forceinline__ int finish_wide2(const Params& p, int r, RowStream<TI
         FrontClaims fc = job >= 0 ? FrontClaims{&J->q2, S, tps, f0, f0} : FrontClaims{own_word, S, tps, S, S};
         w2_pass2<TIn>(rs, rowp, 0, V, bm, pen_on, pen, neg, T, m, yhi, yca, ycb, yda, ydb, wb, ac, ad, w2_cnt, KC, KD,
                       fc, w2_go);
+        taken2 = fc.taken;
         if (job < 0 || wj_wait(&J->done2, S - fc.taken)) break;
         close_job();
         if (tid == 0) { w2_cnt[0] = 0; w2_cnt[1] = 0; }
@@ -2214,18 +2245,38 @@ __device__ __forceinline__ int finish_wide2(const Params& p, int r, RowStream<TI
 #pragma unroll
     for (int v = 0; v < NWAVES; ++v) { WB += w2_s[0][v]; AC += w2_s[1][v]; AD += w2_s[2][v]; }
     uint32_t nc = w2_cnt[0], nd = w2_cnt[1];
-    if (job >= 0) {   // the helpers' sums and window elements
-        WB += ld_dev64(&J->wb);
-        AC += ld_dev64(&J->ac);
-        AD += ld_dev64(&J->ad);
-        const uint32_t gc = ld_dev(&J->nc), gd = ld_dev(&J->nd);
-        if (nc + gc <= (uint32_t)LCAP && nd + gd <= (uint32_t)LCAP) {
-            const u64 *gkc = wj_kc(J), *gkd = wj_kd(J);
-            for (uint32_t j = (uint32_t)tid; j < gc; j += NT) KC[nc + j] = ld_dev64(gkc + j);
-            for (uint32_t j = (uint32_t)tid; j < gd; j += NT) KD[nd + j] = ld_dev64(gkd + j);
+    if (job >= 0) {   // the helpers' sums (a lane per slice) and window elements
+        if (w == 0) {
+            const bool hs = lane < S && lane >= taken2;
+            const u64 sb = hs ? ld_dev64(wj_sums(J, lane)) : 0ull;
+            const u64 sc = hs ? ld_dev64(wj_sums(J, lane) + WJ_S) : 0ull;
+            const u64 sd = hs ? ld_dev64(wj_sums(J, lane) + 2 * WJ_S) : 0ull;
+            const u64 a0 = wave_sum_u64(sb), a1 = wave_sum_u64(sc), a2 = wave_sum_u64(sd);
+            if (lane == 0) { w2_hs[0] = a0; w2_hs[1] = a1; w2_hs[2] = a2; }
         }
-        nc += gc;
-        nd += gd;
+        __syncthreads();
+        WB += w2_hs[0];
+        AC += w2_hs[1];
+        AD += w2_hs[2];
+        // the helpers' window elements after the owner's (a slice's count
+        // above its room counts as more than LCAP: the general path)
+        for (int list = 1; list <= 2; ++list) {
+            uint32_t& n = list == 1 ? nc : nd;
+            u64* K = list == 1 ? KC : KD;
+            if (!slice_counts(list, taken2, (uint32_t)WJ_WINS)) {
+                n = (uint32_t)LCAP + 1u;
+                continue;
+            }
+            if (n + w2_tot <= (uint32_t)LCAP) {
+                for (int j = taken2 * WJ_WINS + tid; j < S * WJ_WINS; j += NT) {
+                    const int sl = j / WJ_WINS, i = j % WJ_WINS;
+                    if ((uint32_t)i < w2_sc[sl])
+                        K[n + w2_so[sl] + i] = ld_dev64((list == 1 ? wj_kc(J, sl) : wj_kd(J, sl)) + i);
+                }
+            }
+            n += w2_tot;
+            __syncthreads();   // (w2_sc, w2_so are read before the next list's counts)
+        }
         close_job();   // (its barrier publishes the lists)
     }
     const u64 W = Wtop + WB;
@@ -2282,19 +2333,26 @@ __device__ __forceinline__ int finish_wide2(const Params& p, int r, RowStream<TI
 // every row's workgroup was resident from the start, p.help).  Nothing is
 // polled when the batch has no row with top-k off, or has only such rows
 // (then no row shares).  Wave 0 reads every job's tag and claims at once
-// (a lane per job); a helper stays with its job while it has slices (its
-// next claim rides with the flush of the last slice).  Its LDS is free: the
-// history bitmap of a job's row is rebuilt here, and each slice's bins,
-// top-list entries and window elements are counted here first, then added
-// to the job's records.
+// (a lane per job), then claims a slice of the chosen pass and reads the
+// job's parameters in the same round trip (a lane per word; they were
+// written before the tag that opened the pass); a helper stays with its
+// pass while it has slices (its next claim rides with the hand-over of the
+// last slice).  Its LDS is free: the slice's words of the row's history
+// bitmap are read from the job, and each slice's bins, top-list entries and
+// window elements are counted here first, then handed over: bins and sums
+// by device-scope atomics, entries and their counts into the slice's own
+// places (no returning atomic).
 template <typename TIn>
 __device__ __forceinline__ void help_rows(const Params& p, unsigned char* smem)
 {
     if constexpr (sizeof(TIn) != 4) {
         return;
     } else {
+        constexpr int NPAR = 17;   // the parameter words: WideJob::r .. pen_on (16), then tps
+        static_assert(offsetof(WideJob, pen_on) - offsetof(WideJob, r) == 4 * (NPAR - 2), "parameter words");
         __shared__ int hc_job, hc_phase, hc_slice, hc_S;
-        __shared__ uint32_t hc_ovf, hc_dummy, hc_cnt[2], hc_base[2], hc_go[2];
+        __shared__ uint32_t hc_par[NPAR], hc_ovf, hc_dummy, hc_cnt[2], hc_seg[NWAVES];
+        __shared__ u64 hc_s[3][NWAVES];
         if (p.B <= NT) {
             const uint32_t nw = wide_rows_counted();
             if (nw == 0u || nw >= (uint32_t)p.B) return;
@@ -2307,7 +2365,6 @@ __device__ __forceinline__ void help_rows(const Params& p, unsigned char* smem)
         uint32_t* ci = (uint32_t*)(smem + KF_CI);
         u64* KC = (u64*)(smem + W2_KC);
         u64* KD = (u64*)(smem + W2_KD);
-        int built = -1;   // the job whose row's history bitmap is in bm
         RowStream<TIn> rs((const TIn*)p.logits, 0, false);
         int j = -1, phase = 0, s = -1, S = 0;   // the slice in hand (s >= 0)
         for (int idle = 0; idle < WJ_SPIN;) {
@@ -2328,18 +2385,26 @@ __device__ __forceinline__ void help_rows(const Params& p, unsigned char* smem)
                     const u64 om = __ballot(open), lm = __ballot(live);
                     int cmd = -2, cph = 0, cs = -1, cS = 0;
                     if (om) {
-                        // this workgroup's last job first, then the others from blockIdx mod WJ_NJOB
+                        // this workgroup's last job first, else open job number
+                        // blockIdx mod (open jobs), so that the helpers spread evenly
                         int pick = (j >= 0 && ((om >> j) & 1u)) ? j : -1;
-                        for (int i = 0; i < WJ_NJOB && pick < 0; ++i) {
-                            const int l = ((int)blockIdx.x + i) % WJ_NJOB;
-                            if ((om >> l) & 1u) pick = l;
+                        if (pick < 0) {
+                            int nth = (int)(blockIdx.x % (unsigned)__builtin_popcountll(om));
+                            u64 m = om;
+                            for (; nth > 0; --nth) m &= m - 1ull;
+                            pick = __builtin_ctzll(m);
                         }
                         cph = __builtin_amdgcn_readlane((int)ph, pick);
                         cS = __builtin_amdgcn_readlane((int)Sl, pick);
-                        if (lane == 0) {
-                            WideJob* Jp = wj_job(p.wj, pick);
-                            cs = wj_claim_back(cph == 1 ? &Jp->q1 : &Jp->q2, cS);
-                        }
+                        WideJob* Jp = wj_job(p.wj, pick);
+                        // the claim (lane 0) and the parameters (a lane per word) together
+                        uint32_t got = 0;
+                        if (lane == 0) got = atomicAdd(cph == 1 ? &Jp->q1 : &Jp->q2, 1u << 16);
+                        uint32_t pw = 0;
+                        if (lane < NPAR)
+                            pw = ld_dev(lane < NPAR - 1 ? (const uint32_t*)&Jp->r + lane : &Jp->tps);
+                        if (lane < NPAR) hc_par[lane] = pw;
+                        cs = (got & 0xFFFFu) + (got >> 16) < (uint32_t)cS ? cS - 1 - (int)(got >> 16) : -1;
                         cmd = pick;   // (a refused claim: scan again at once)
                     } else if (lm && p.help) {
                         cmd = -1;     // jobs pending: wait
@@ -2363,10 +2428,12 @@ __device__ __forceinline__ void help_rows(const Params& p, unsigned char* smem)
             }
             idle = 0;
             WideJob* J = wj_job(p.wj, j);
-            // the job's parameters (read at device scope: the owner wrote them through)
-            const int r = (int)ld_dev((const uint32_t*)&J->r), tps = (int)ld_dev(&J->tps);
-            const bool neg = ld_dev(&J->neg) != 0u, pen_on = ld_dev(&J->pen_on) != 0u;
-            const float T = ld_devf(&J->T), pen = ld_devf(&J->pen), yhi = ld_devf(&J->yhi);
+            const int r = (int)hc_par[0], h0 = (int)hc_par[1], h1 = (int)hc_par[2];
+            const float T = u2f(hc_par[4]), pen = u2f(hc_par[5]), yhi = u2f(hc_par[6]);
+            const bool neg = hc_par[14] != 0u, pen_on = hc_par[15] != 0u;
+            const int tps = (int)hc_par[16];
+            (void)h0;
+            (void)h1;
             if ((unsigned)r >= (unsigned)p.B || tps < 1) {   // (not a record of this call: leave it)
                 s = -1;
                 j = -1;
@@ -2376,30 +2443,23 @@ __device__ __forceinline__ void help_rows(const Params& p, unsigned char* smem)
             const int L = tps * FTILE;
             const int s0 = s * L < V ? s * L : V;
             const int n = (s0 + L < V ? s0 + L : V) - s0;
-            if (pen_on && built != j) {   // the row's history (its ids were checked by the owner)
-                const int h0 = (int)ld_dev((const uint32_t*)&J->h0), h1 = (int)ld_dev((const uint32_t*)&J->h1);
-                const int words = (V + 31) >> 5;
-                for (int wd = tid; wd < words; wd += NT) bm[wd] = 0;
-                __syncthreads();
-                for (int h = h0 + tid; h < h1; h += NT) {
-                    const int id = p.hids[h];
-                    if (id >= 0 && id < V) atomicOr(&bm[id >> 5], 1u << (id & 31));
-                }
-                __syncthreads();
-                built = j;
+            if (pen_on) {   // the slice's words of the row's history bitmap (the owner wrote them)
+                const int w0 = s0 >> 5, nw = (n + 31) >> 5;
+                const uint32_t* gm = wj_bm(J);
+                for (int i = tid; i < nw; i += NT) bm[w0 + i] = ld_dev(gm + w0 + i);
             }
             NoClaims mine{S};
             uint32_t* q;
             uint32_t* done;
             if (phase == 1) {
-                const float ylo = ld_devf(&J->ylo), scale = ld_devf(&J->scale);
+                const float ylo = u2f(hc_par[7]), scale = u2f(hc_par[8]);
                 for (int b = tid; b < 2048; b += NT) CH[b] = 0;
                 if (tid == 0) hc_ovf = 0;
                 __syncthreads();
                 uint32_t cw = 0;
                 float fmx = -INFINITY, fmn = INFINITY;
                 w2_pass1<TIn>(rs, rowp, s0, n, bm, pen_on, pen, neg, yhi, ylo, scale, CH, ck + w * FSEG,
-                              ci + w * FSEG, cw, fmx, fmn, &hc_ovf, &hc_dummy, mine, hc_go);
+                              ci + w * FSEG, cw, fmx, fmn, &hc_ovf, &hc_dummy, mine, hc_go_dummy(), false);
                 uint32_t omax, omin;
                 if (fmx != fmx) {
                     omax = 0xFFFFFFFFu;
@@ -2408,58 +2468,58 @@ __device__ __forceinline__ void help_rows(const Params& p, unsigned char* smem)
                     omax = neg ? selkey(fmn, true) : selkey(fmx, false);
                     omin = neg ? selkey(fmx, true) : selkey(fmn, false);
                 }
-                const Reduced rw = block_reduce(omax, omin, 0u);   // (its barriers publish CH and the segments)
+                if (lane == 0) hc_seg[w] = cw;
+                const Reduced rw = block_reduce(omax, omin, 0u);   // (its barriers publish CH, the segments, hc_seg)
                 uint32_t* gb = wj_bins(J);
                 for (int b = tid; b < 2048; b += NT) {
                     const uint32_t c = CH[b];
                     if (c) atomicAdd(gb + b, c);
                 }
-                // this wave's top-list entries after the others' (one atomic per wave)
-                uint32_t base = 0;
-                if (lane == 0 && cw) base = atomicAdd(&J->ntop, cw);
-                base = (uint32_t)__builtin_amdgcn_readlane((int)base, 0);
-                u64* gt = wj_top(J);
+                // the slice's top-list entries, the waves' segments in order
+                uint32_t base = 0, tot = 0;
+#pragma unroll
+                for (int v = 0; v < NWAVES; ++v) {
+                    base += v < w ? hc_seg[v] : 0u;
+                    tot += hc_seg[v];
+                }
+                u64* gt = wj_top(J, s);
                 const uint32_t* wck = ck + w * FSEG;
                 const uint32_t* wci = ci + w * FSEG;
                 for (uint32_t i = (uint32_t)lane; i < cw; i += 64)
-                    if (base + i < (uint32_t)WJ_TOP) put_dev64(gt + base + i, ((u64)wck[i] << 32) | wci[i]);
+                    if (base + i < (uint32_t)WJ_TOPS) put_dev64(gt + base + i, ((u64)wck[i] << 32) | wci[i]);
                 if (tid == 0) {
                     atomicMax(&J->gmax, rw.max);
                     atomicMin(&J->gmin, rw.min);
                     if (hc_ovf) put_dev32(&J->ovf, 1u);
+                    put_dev32(wj_cnt(J, 0) + s, tot);   // (above WJ_TOPS: the owner takes the general path)
                 }
-                if (lane == 0 && base + cw > (uint32_t)WJ_TOP) put_dev32(&J->ovf, 1u);
                 q = &J->q1;
                 done = &J->done1;
             } else {
-                const float m = ld_devf(&J->m), yca = ld_devf(&J->yca), ycb = ld_devf(&J->ycb);
-                const float yda = ld_devf(&J->yda), ydb = ld_devf(&J->ydb);
+                const float m = u2f(hc_par[9]), yca = u2f(hc_par[10]), ycb = u2f(hc_par[11]);
+                const float yda = u2f(hc_par[12]), ydb = u2f(hc_par[13]);
                 if (tid == 0) { hc_cnt[0] = 0; hc_cnt[1] = 0; }
                 __syncthreads();
                 u64 wb = 0, ac = 0, ad = 0;
                 w2_pass2<TIn>(rs, rowp, s0, n, bm, pen_on, pen, neg, T, m, yhi, yca, ycb, yda, ydb, wb, ac, ad, hc_cnt,
-                              KC, KD, mine, hc_go);
+                              KC, KD, mine, hc_go_dummy());
                 const u64 a0 = wave_sum_u64(wb), a1 = wave_sum_u64(ac), a2 = wave_sum_u64(ad);
-                if (lane == 0) {
-                    atomicAdd(&J->wb, a0);
-                    atomicAdd(&J->ac, a1);
-                    atomicAdd(&J->ad, a2);
+                if (lane == 0) { hc_s[0][w] = a0; hc_s[1][w] = a1; hc_s[2][w] = a2; }
+                __syncthreads();   // (the lists and the waves' sums are complete)
+                const uint32_t nc = hc_cnt[0], nd = hc_cnt[1];
+                u64 *gkc = wj_kc(J, s), *gkd = wj_kd(J, s);
+                for (uint32_t i = (uint32_t)tid; i < nc && i < (uint32_t)WJ_WINS; i += NT) put_dev64(gkc + i, KC[i]);
+                for (uint32_t i = (uint32_t)tid; i < nd && i < (uint32_t)WJ_WINS; i += NT) put_dev64(gkd + i, KD[i]);
+                if (tid == 0) {   // (above WJ_WINS: the owner takes the general path)
+                    put_dev32(wj_cnt(J, 1) + s, nc);
+                    put_dev32(wj_cnt(J, 2) + s, nd);
+                    u64 tb = 0, tc = 0, td = 0;
+#pragma unroll
+                    for (int v = 0; v < NWAVES; ++v) { tb += hc_s[0][v]; tc += hc_s[1][v]; td += hc_s[2][v]; }
+                    put_dev64(wj_sums(J, s), tb);
+                    put_dev64(wj_sums(J, s) + WJ_S, tc);
+                    put_dev64(wj_sums(J, s) + 2 * WJ_S, td);
                 }
-                __syncthreads();   // (the lists are complete)
-                const uint32_t nc = hc_cnt[0] < (uint32_t)LCAP ? hc_cnt[0] : (uint32_t)LCAP;
-                const uint32_t nd = hc_cnt[1] < (uint32_t)LCAP ? hc_cnt[1] : (uint32_t)LCAP;
-                if (tid == 0) {
-                    // (a count past LCAP makes the owner's total exceed it: the owner then takes the general path)
-                    hc_base[0] = hc_cnt[0] ? atomicAdd(&J->nc, hc_cnt[0]) : 0u;
-                    hc_base[1] = hc_cnt[1] ? atomicAdd(&J->nd, hc_cnt[1]) : 0u;
-                }
-                __syncthreads();
-                const uint32_t bc = hc_base[0], bd = hc_base[1];
-                u64 *gkc = wj_kc(J), *gkd = wj_kd(J);
-                for (uint32_t i = (uint32_t)tid; i < nc; i += NT)
-                    if (bc + i < (uint32_t)WJ_WIN) put_dev64(gkc + bc + i, KC[i]);
-                for (uint32_t i = (uint32_t)tid; i < nd; i += NT)
-                    if (bd + i < (uint32_t)WJ_WIN) put_dev64(gkd + bd + i, KD[i]);
                 q = &J->q2;
                 done = &J->done2;
             }

@@ -10,6 +10,7 @@
 #include <stdint.h>
 
 #include "mxs_device.h"
+#include "mxs_sampler.h"   // (MXS_MAX_VOCAB)
 
 namespace mxs {
 
@@ -74,16 +75,20 @@ static_assert(SPLIT_MAX_B * (SPLIT_SLICES / SPLIT_MAX_B) <= SPLIT_SLICES && 4 * 
 // tiles; workgroups that have finished their own rows take slices from the
 // back while the owner streams from the front, and hand their results over
 // through the workspace, the owner merges them with its own.  The records:
-// WJ_NJOB jobs (row r uses job r mod WJ_NJOB), each a header of WJ_HDR
-// bytes, the helpers' bin counts (2048 u32), top-list entries (WJ_TOP u64)
-// and window elements (2 x WJ_WIN u64).  Every record carries the call's
-// epoch, so a call needs no reset of the previous call's state.
+// WJ_NJOB jobs, each a header of WJ_HDR bytes, the helpers' bin counts
+// (2048 u32), per slice up to WJ_TOPS top-list entries and WJ_WINS elements
+// of each of the two windows (u64), the slices' counts of these (3 x WJ_S
+// u32), the row's history bitmap (WJ_BMW u32, written once by the owner)
+// and the slices' pass-2 sums (3 x WJ_S u64).  Every record carries the call's epoch, so a call needs no reset
+// of the previous call's state.
 constexpr int WJ_NJOB = 16;
 constexpr int WJ_S = 32;
-constexpr int WJ_TOP = 2048;
-constexpr int WJ_WIN = 4096;
+constexpr int WJ_TOPS = 64;
+constexpr int WJ_WINS = 128;
+constexpr int WJ_BMW = MXS_MAX_VOCAB / 32;
 constexpr size_t WJ_HDR = 256;
-constexpr size_t WJ_JOB_BYTES = WJ_HDR + 4 * 2048 + 8 * (size_t)WJ_TOP + 2 * 8 * (size_t)WJ_WIN;
+constexpr size_t WJ_JOB_BYTES = WJ_HDR + 4 * 2048 + 8 * (size_t)WJ_S * WJ_TOPS + 2 * 8 * (size_t)WJ_S * WJ_WINS +
+                                4 * 3 * (size_t)WJ_S + 4 * (size_t)WJ_BMW + 8 * 3 * (size_t)WJ_S;
 constexpr int WJ_OWN = 512;   // then a 64-byte line per row (rows r mod WJ_OWN), Params::wown
 constexpr size_t WJ_BYTES = WJ_NJOB * WJ_JOB_BYTES + 64 * (size_t)WJ_OWN;
 
