@@ -1815,6 +1815,18 @@ __device__ __forceinline__ void w2_pass1(RowStream<TIn>& rs, const TIn* rowp, in
         });
 }
 
+// fl32(x / T) from rT = RN64(1 / T): x * rT in binary64 is within 2^-52
+// (relative) of x / T, and x / T is never a binary32 rounding boundary (an
+// odd 25-bit midpoint times T needs more than 24 significant bits) nor
+// nearer to one than 2^-49 (relative) while its quotient is normal, so the
+// product rounds to binary32 exactly as the IEEE quotient does.  A
+// subnormal quotient may differ by its last bit; pass 2 uses it only in
+// d = fl32(l - m), which it leaves unchanged when m = 0 or |m| >= 2^-101
+// (the row's maximum; finish_wide2 checks).  Infinities, zeros and NaN
+// pass through as in the division.  Two conversions and one binary64
+// multiply in place of the division's reciprocal and refinement steps.
+__device__ __forceinline__ float div_by_rT(float x, double rT) { return (float)((double)x * rT); }
+
 // Pass 2: the exact masses of the elements below yhi summed (wb), and those
 // at or above ycb (ac) and ydb (ad); the elements of the windows [yca, ycb)
 // and [yda, ydb) listed in KC and KD (counts in cnt[0], cnt[1]).  fc as
@@ -1822,7 +1834,8 @@ __device__ __forceinline__ void w2_pass1(RowStream<TIn>& rs, const TIn* rowp, in
 template <typename TIn, class FC>
 __device__ __forceinline__ void w2_pass2(RowStream<TIn>& rs, const TIn* rowp, int s0, int n, const uint32_t* bm,
                                          bool pen_on, float pen,
-                                         bool neg, float T, float m, float yhi, float yca, float ycb, float yda,
+                                         bool neg, float T, double rT, float m, float yhi, float yca, float ycb,
+                                         float yda,
                                          float ydb, u64& wb, u64& ac, u64& ad, uint32_t* cnt, u64* KC, u64* KD,
                                          FC& fc, uint32_t* go)
 {
@@ -1834,7 +1847,7 @@ __device__ __forceinline__ void w2_pass2(RowStream<TIn>& rs, const TIn* rowp, in
     rs.run_pen_val(pen_on ? bm + (s0 >> 5) : bm, pen_on, pen,
         [&](int i, int, float x) {
             const float y = yv(x);
-            const float l = x / T;
+            const float l = div_by_rT(x, rT);
             const u64 wgt = y >= yhi ? 0ull : count_mass(1u, l - m);
             wb += wgt;
             ac += y >= ycb ? wgt : 0ull;
@@ -2098,6 +2111,9 @@ __device__ __forceinline__ int finish_wide2(const Params& p, int r, RowStream<TI
     if (!isfinite(m)) { close_job(); st = MXS_ROW_NONFINITE; tok = -1; return 1; }
     if (top_p < 1.0f && !(top_p > 0.0f)) { close_job(); st = MXS_ROW_EMPTY_NUCLEUS; tok = -1; return 1; }
     if (w2_ovf || govf || ntop + gtop > (uint32_t)TL_CAP) { close_job(); return 0; }
+    // (pass 2's quotients by rT: exact in d = l - m for these m; see div_by_rT)
+    if (m != 0.0f && __builtin_fabsf(m) < 0x1p-101f) { close_job(); return 0; }
+    const double rT = 1.0 / (double)T;
 
     // the top list's keys and exact masses (the helpers' entries after the owner's)
     u64 part = 0;
@@ -2223,11 +2239,11 @@ __device__ __forceinline__ int finish_wide2(const Params& p, int r, RowStream<TI
     }
     if constexpr (!SH) {
         NoClaims fc{S};
-        w2_pass2<TIn>(rs, rowp, 0, V, bm, pen_on, pen, neg, T, m, yhi, yca, ycb, yda, ydb, wb, ac, ad, w2_cnt, KC, KD,
+        w2_pass2<TIn>(rs, rowp, 0, V, bm, pen_on, pen, neg, T, rT, m, yhi, yca, ycb, yda, ydb, wb, ac, ad, w2_cnt, KC, KD,
                       fc, w2_go);
     } else for (;;) {   // (as for pass 1)
         FrontClaims fc = job >= 0 ? FrontClaims{&J->q2, S, tps, f0, f0} : FrontClaims{own_word, S, tps, S, S};
-        w2_pass2<TIn>(rs, rowp, 0, V, bm, pen_on, pen, neg, T, m, yhi, yca, ycb, yda, ydb, wb, ac, ad, w2_cnt, KC, KD,
+        w2_pass2<TIn>(rs, rowp, 0, V, bm, pen_on, pen, neg, T, rT, m, yhi, yca, ycb, yda, ydb, wb, ac, ad, w2_cnt, KC, KD,
                       fc, w2_go);
         taken2 = fc.taken;
         if (job < 0 || wj_wait(&J->done2, S - fc.taken)) break;
@@ -2501,7 +2517,7 @@ __device__ __forceinline__ void help_rows(const Params& p, unsigned char* smem)
                 if (tid == 0) { hc_cnt[0] = 0; hc_cnt[1] = 0; }
                 __syncthreads();
                 u64 wb = 0, ac = 0, ad = 0;
-                w2_pass2<TIn>(rs, rowp, s0, n, bm, pen_on, pen, neg, T, m, yhi, yca, ycb, yda, ydb, wb, ac, ad, hc_cnt,
+                w2_pass2<TIn>(rs, rowp, s0, n, bm, pen_on, pen, neg, T, 1.0 / (double)T, m, yhi, yca, ycb, yda, ydb, wb, ac, ad, hc_cnt,
                               KC, KD, mine, hc_go_dummy());
                 const u64 a0 = wave_sum_u64(wb), a1 = wave_sum_u64(ac), a2 = wave_sum_u64(ad);
                 if (lane == 0) { hc_s[0][w] = a0; hc_s[1][w] = a1; hc_s[2][w] = a2; }
