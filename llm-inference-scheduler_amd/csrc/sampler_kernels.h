@@ -2762,6 +2762,11 @@ __device__ __forceinline__ bool finish_counts(const Params& p, int r, RowStream<
         m = mh > m ? mh : m;
     }
     if (!__builtin_isfinite(m)) { st = MXS_ROW_NONFINITE; tok = -1; return true; }
+    // (the chunk masses take their quotients by rT: exact in d = l - m for
+    // these m, see div_by_rT)
+    if (m != 0.0f && __builtin_fabsf(m) < 0x1p-101f) { restore(); return false; }
+    const double rT = 1.0 / (double)T;
+    auto val_q = [&](uint32_t R) { return div_by_rT(VecIO<__half>::h2f(R ^ (R < 0x8000u ? XA : XB)), rT); };
 
     // each history value's place: the last rank whose value is >= it, from
     // the rank of fp16(l * T) (the place itself or a neighbour)
@@ -2801,8 +2806,8 @@ __device__ __forceinline__ bool finish_counts(const Params& p, int r, RowStream<
             if (__ballot((wd.x | wd.y) != 0u)) {
                 const uint32_t R0 = (uint32_t)(RCH * c) + 4u * (uint32_t)lane;
                 const uint32_t k0 = wd.x & 0xFFFFu, k1 = wd.x >> 16, k2 = wd.y & 0xFFFFu, k3 = wd.y >> 16;
-                acc = count_mass(k0, val_fin(R0) - m) + count_mass(k1, val_fin(R0 + 1u) - m) +
-                      count_mass(k2, val_fin(R0 + 2u) - m) + count_mass(k3, val_fin(R0 + 3u) - m);
+                acc = count_mass(k0, val_q(R0) - m) + count_mass(k1, val_q(R0 + 1u) - m) +
+                      count_mass(k2, val_q(R0 + 2u) - m) + count_mass(k3, val_q(R0 + 3u) - m);
                 csum += k0 + k1 + k2 + k3;
                 // (RK_NINF is a multiple of 4: the ranks above it are NaN values)
                 nanb |= R0 > RK_NINF ? (wd.x | wd.y) : (R0 == RK_NINF ? (k1 | wd.y) : 0u);
