@@ -307,7 +307,11 @@ def main():
     w = make_workload(args.workload, B=args.batch)
     d = w.to_device(dev)
     s = Sampler(w.B, w.V, dev)
-    run = lambda: s.run(**d)
+    # the flag a serving engine sets from its host-side parameters
+    # (mi355x_sampler.shares_rows): rows with top-k off mixed with others
+    off = (w.temperature != 0) & ((w.top_k <= 0) | (w.top_k >= w.V))
+    share_rows = bool(off.any() and not off.all())
+    run = lambda: s.run(**d, share_rows=share_rows)
 
     log(f"[bench] warmup {args.warmup}")
     for _ in range(args.warmup):
@@ -425,6 +429,7 @@ def main():
                 "zipf_k0": "the zipf batch with top_k=0 on every 32nd row (8 rows)",
             }[args.workload] if args.batch is None else f"{args.workload} with B={w.B}",
             "B": int(w.B), "V": int(w.V),
+            "share_rows": share_rows,
         },
         "hbm_gbps": achieved,
         "pct_of_hbm_peak": 100.0 * achieved / HBM_PEAK_GBPS,

@@ -36,6 +36,18 @@ enum mxs_dtype {
     MXS_DTYPE_F16 = 1
 };
 
+/*
+ * Or'ed into the dtype argument of the sampling calls: the batch may mix
+ * rows with top-k off (top_k <= 0 or >= V, temperature not 0) with other
+ * rows.  For fp32 batches of more than 64 rows, the first 16 such rows then
+ * share their two reads of the logits with the workgroups that finished
+ * their own rows (the caller knows each row's parameters when it builds
+ * them; sample_requests sets the flag for such batches).  Results are the
+ * same with and without it; without it, a launch carries none of the
+ * sharing code, which costs the other rows about a microsecond.
+ */
+#define MXS_FLAG_SHARE_ROWS 0x100
+
 /* Return codes of the calls below. */
 enum mxs_status {
     MXS_OK = 0,

@@ -119,6 +119,8 @@ int sample_impl(const void* logits, int dtype, int B, int V, int64_t ld,
 {
     if (B < 0 || V <= 0) return MXS_ERR_INVALID_ARGUMENT;
     if (V > MXS_MAX_VOCAB) return MXS_ERR_VOCAB_TOO_LARGE;
+    const bool share = (dtype & MXS_FLAG_SHARE_ROWS) != 0;
+    dtype &= ~MXS_FLAG_SHARE_ROWS;
     if (dtype != MXS_DTYPE_F32 && dtype != MXS_DTYPE_F16) return MXS_ERR_INVALID_ARGUMENT;
     if (B == 0) return MXS_OK;
     if (!logits || !temperature || !top_k || !top_p || !penalty || !out_tokens || !workspace)
@@ -160,7 +162,7 @@ int sample_impl(const void* logits, int dtype, int B, int V, int64_t ld,
         p.G = split_slices(B);
         p.sl_hdr = (const uint32_t*)workspace;
         p.sl_ent = (const uint32_t*)((const char*)workspace + SL_HDR_BYTES);
-    } else {
+    } else if (share && dtype == MXS_DTYPE_F32) {
         p.wj = (unsigned char*)workspace + WJ_OFF;
         unsigned int e = ++g_epoch;
         if (e == 0) e = ++g_epoch;
@@ -171,6 +173,7 @@ int sample_impl(const void* logits, int dtype, int B, int V, int64_t ld,
     bool lds_error = false;
     hipError_t e;
     if (p.sl_hdr) e = dtype == MXS_DTYPE_F32 ? launch_split<float>(p, s, lds_error) : launch_split<__half>(p, s, lds_error);
+    else if (p.wj) e = launch_fused_share(p, s, lds_error);
     else e = dtype == MXS_DTYPE_F32 ? launch_fused<float>(p, s, lds_error) : launch_fused<__half>(p, s, lds_error);
     if (e == hipSuccess) return MXS_OK;
     return lds_error ? MXS_ERR_LDS_LIMIT : MXS_ERR_HIP;

@@ -51,7 +51,7 @@ void sample_common(torch::Tensor logits, torch::Tensor temperature, torch::Tenso
                    std::optional<torch::Tensor> hist_offsets, std::optional<torch::Tensor> hist_ids,
                    std::optional<torch::Tensor> uniforms, torch::Tensor out_tokens,
                    std::optional<torch::Tensor> out_status, std::optional<torch::Tensor> out_probs,
-                   const std::optional<torch::Tensor>& row_best, torch::Tensor workspace)
+                   const std::optional<torch::Tensor>& row_best, torch::Tensor workspace, int64_t flags)
 {
     TORCH_CHECK(logits.is_cuda(), "logits must be on a GPU device");
     TORCH_CHECK(logits.dim() == 2, "logits must be [B, V]");
@@ -61,6 +61,8 @@ void sample_common(torch::Tensor logits, torch::Tensor temperature, torch::Tenso
     if (logits.scalar_type() == torch::kFloat32) dtype = MXS_DTYPE_F32;
     else if (logits.scalar_type() == torch::kFloat16) dtype = MXS_DTYPE_F16;
     else TORCH_CHECK(false, "logits must be float32 or float16, got ", logits.scalar_type());
+    TORCH_CHECK((flags & ~(int64_t)MXS_FLAG_SHARE_ROWS) == 0, "unknown flags ", flags);
+    dtype |= (int)flags;
 
     check_dev(temperature, logits, "temperature", torch::kFloat32, B);
     check_dev(top_k, logits, "top_k", torch::kInt32, B);
@@ -116,10 +118,10 @@ void sample(torch::Tensor logits, torch::Tensor temperature, torch::Tensor top_k
             std::optional<torch::Tensor> hist_offsets, std::optional<torch::Tensor> hist_ids,
             std::optional<torch::Tensor> uniforms, torch::Tensor out_tokens,
             std::optional<torch::Tensor> out_status, std::optional<torch::Tensor> out_probs,
-            torch::Tensor workspace)
+            torch::Tensor workspace, int64_t flags)
 {
     sample_common(logits, temperature, top_k, top_p, penalty, hist_offsets, hist_ids, uniforms, out_tokens,
-                  out_status, out_probs, std::nullopt, workspace);
+                  out_status, out_probs, std::nullopt, workspace, flags);
 }
 
 // mxs_sample_head: greedy rows without a penalty take their token from
@@ -129,11 +131,11 @@ void sample_head(torch::Tensor logits, torch::Tensor temperature, torch::Tensor 
                  std::optional<torch::Tensor> hist_offsets, std::optional<torch::Tensor> hist_ids,
                  std::optional<torch::Tensor> uniforms, torch::Tensor out_tokens,
                  std::optional<torch::Tensor> out_status, std::optional<torch::Tensor> out_probs,
-                 torch::Tensor row_best, torch::Tensor workspace)
+                 torch::Tensor row_best, torch::Tensor workspace, int64_t flags)
 {
     check_dev(row_best, logits, "row_best", torch::kInt64, logits.dim() == 2 ? logits.size(0) : -1);
     sample_common(logits, temperature, top_k, top_p, penalty, hist_offsets, hist_ids, uniforms, out_tokens,
-                  out_status, out_probs, row_best, workspace);
+                  out_status, out_probs, row_best, workspace, flags);
 }
 
 // logits = hidden . weight^T and the rows' packed maxima (mxs_lm_head)
@@ -167,7 +169,7 @@ void sample_ranges(torch::Tensor logits, torch::Tensor temperature, torch::Tenso
                    torch::Tensor hist_begin, torch::Tensor hist_end, torch::Tensor hist_ids,
                    std::optional<torch::Tensor> uniforms, torch::Tensor out_tokens,
                    std::optional<torch::Tensor> out_status, std::optional<torch::Tensor> out_probs,
-                   torch::Tensor workspace)
+                   torch::Tensor workspace, int64_t flags)
 {
     TORCH_CHECK(logits.is_cuda(), "logits must be on a GPU device");
     TORCH_CHECK(logits.dim() == 2, "logits must be [B, V]");
@@ -177,6 +179,8 @@ void sample_ranges(torch::Tensor logits, torch::Tensor temperature, torch::Tenso
     if (logits.scalar_type() == torch::kFloat32) dtype = MXS_DTYPE_F32;
     else if (logits.scalar_type() == torch::kFloat16) dtype = MXS_DTYPE_F16;
     else TORCH_CHECK(false, "logits must be float32 or float16, got ", logits.scalar_type());
+    TORCH_CHECK((flags & ~(int64_t)MXS_FLAG_SHARE_ROWS) == 0, "unknown flags ", flags);
+    dtype |= (int)flags;
 
     check_dev(temperature, logits, "temperature", torch::kFloat32, B);
     check_dev(top_k, logits, "top_k", torch::kInt32, B);
@@ -218,13 +222,14 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m)
     m.def("sample", &sample, "sample one token per row (see mxs_sampler.h)",
           py::arg("logits"), py::arg("temperature"), py::arg("top_k"), py::arg("top_p"),
           py::arg("penalty"), py::arg("hist_offsets"), py::arg("hist_ids"), py::arg("uniforms"),
-          py::arg("out_tokens"), py::arg("out_status"), py::arg("out_probs"), py::arg("workspace"));
+          py::arg("out_tokens"), py::arg("out_status"), py::arg("out_probs"), py::arg("workspace"),
+          py::arg("flags") = 0);
     m.def("sample_head", &sample_head,
           "sample with the LM head's row maxima (see mxs_sample_head)",
           py::arg("logits"), py::arg("temperature"), py::arg("top_k"), py::arg("top_p"),
           py::arg("penalty"), py::arg("hist_offsets"), py::arg("hist_ids"), py::arg("uniforms"),
           py::arg("out_tokens"), py::arg("out_status"), py::arg("out_probs"), py::arg("row_best"),
-          py::arg("workspace"));
+          py::arg("workspace"), py::arg("flags") = 0);
     m.def("lm_head", &lm_head, "logits = hidden . weight^T with the rows' packed maxima (mxs_lm_head)",
           py::arg("hidden"), py::arg("weight"), py::arg("out_logits"), py::arg("out_best"));
     m.def("sample_ranges", &sample_ranges,
@@ -232,5 +237,6 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m)
           py::arg("logits"), py::arg("temperature"), py::arg("top_k"), py::arg("top_p"),
           py::arg("penalty"), py::arg("hist_begin"), py::arg("hist_end"), py::arg("hist_ids"),
           py::arg("uniforms"), py::arg("out_tokens"), py::arg("out_status"), py::arg("out_probs"),
-          py::arg("workspace"));
+          py::arg("workspace"), py::arg("flags") = 0);
+    m.attr("FLAG_SHARE_ROWS") = (int)MXS_FLAG_SHARE_ROWS;
 }

@@ -3287,7 +3287,7 @@ __device__ __forceinline__ bool finish_counts_as(const Params& p, int r, RowStre
 // One row's chain in one workgroup.  SPLIT: the row's slices (slice_row)
 // are done, and their candidates may replace the row's stream; the
 // instance without it has none of that code.
-template <typename TIn, bool SPLIT>
+template <typename TIn, bool SPLIT, bool SHARE = false>
 __device__ __forceinline__ void fused_row(const Params p, const int r, unsigned char* smem)
 {
     uint32_t* ck = (uint32_t*)(smem + KF_CK);   // candidate selection keys
@@ -3328,7 +3328,7 @@ __device__ __forceinline__ void fused_row(const Params p, const int r, unsigned 
     // among the first NT rows, each wave counting 64; read with the parameters
     int kb = 0;
     float tb = 0.0f;
-    if constexpr (!SPLIT) {
+    if constexpr (!SPLIT && SHARE) {
         const int i = tid < p.B ? tid : 0;
         kb = p.K[i];
         tb = p.T[i];
@@ -3362,7 +3362,7 @@ __device__ __forceinline__ void fused_row(const Params p, const int r, unsigned 
     const int hv0 = __builtin_amdgcn_readlane((int)pv, 4);
     const int hv1 = __builtin_amdgcn_readlane((int)pv, 5);
     const float uv = __builtin_bit_cast(float, (uint32_t)__builtin_amdgcn_readlane((int)pv, 6));
-    if constexpr (!SPLIT) {
+    if constexpr (!SPLIT && SHARE) {
         const bool wd = sizeof(TIn) == 4 && tid < p.B && tb != 0.0f && tb == tb && (kb <= 0 || kb >= V) &&
                         V >= FAST_MIN_V;
         const u64 wm = __ballot(wd);
@@ -3962,7 +3962,7 @@ __device__ __forceinline__ void fused_row(const Params p, const int r, unsigned 
                 if (!overflow) fix_up();
             }
         } else if (mode == MODE_LARGE && (k <= 0 || k >= V) && V >= FAST_MIN_V &&
-                   (wide2 = finish_wide2<TIn, !SPLIT>(p, r, rs, T, neg, top_p, u, pen, pen_on, bm, sx, se0, h0, h1, smem, hist,
+                   (wide2 = finish_wide2<TIn, !SPLIT && SHARE>(p, r, rs, T, neg, top_p, u, pen, pen_on, bm, sx, se0, h0, h1, smem, hist,
                                               rd, tok, st)) >= 0) {
             // top-k off, two passes (done, or rd holds the extremes for the general path)
             have_rd = true;
@@ -4088,16 +4088,21 @@ __device__ __forceinline__ void fused_row(const Params p, const int r, unsigned 
     }
 }
 
-// Batches above SPLIT_MAX_B rows: one workgroup per row; then it helps
-// with the top-k-off rows still running (help_rows).
-template <typename TIn>
+// Batches above SPLIT_MAX_B rows: one workgroup per row.  SHARE (the
+// caller's flag MXS_FLAG_SHARE_ROWS, fp32): rows with top-k off share their
+// passes, and every workgroup then helps with those still running
+// (help_rows).  The instance without it has none of that code: its
+// presence alone costs the other rows about a microsecond.
+template <typename TIn, bool SHARE>
 __global__ __launch_bounds__(NT, 1) void k_fused(Params p)
 {
     extern __shared__ __align__(16) unsigned char smem[];
-    fused_row<TIn, false>(p, (int)blockIdx.x, smem);
-    if (p.wj) {
-        __syncthreads();   // (the row's LDS is free)
-        help_rows<TIn>(p, smem);
+    fused_row<TIn, false, SHARE>(p, (int)blockIdx.x, smem);
+    if constexpr (SHARE) {
+        if (p.wj) {
+            __syncthreads();   // (the row's LDS is free)
+            help_rows<TIn>(p, smem);
+        }
     }
 }
 

@@ -98,6 +98,8 @@ constexpr size_t WJ_BYTES = WJ_NJOB * WJ_JOB_BYTES + 64 * (size_t)WJ_OWN;
 // the kernels' LDS limit (lds_error is then set).
 template <typename TIn>
 hipError_t launch_fused(const Params& p, hipStream_t s, bool& lds_error);
+// k_fused with shared top-k-off rows (fp32; k_f32_share.hip)
+hipError_t launch_fused_share(const Params& p, hipStream_t s, bool& lds_error);
 template <typename TIn>
 hipError_t launch_split(const Params& p, hipStream_t s, bool& lds_error);
 

@@ -33,7 +33,8 @@ def sample_batch(logits: torch.Tensor, temperature: torch.Tensor, top_k: torch.T
                  uniforms: Optional[torch.Tensor] = None,
                  out_probs: Optional[torch.Tensor] = None,
                  return_status: bool = False,
-                 row_best: Optional[torch.Tensor] = None):
+                 row_best: Optional[torch.Tensor] = None,
+                 share_rows: bool = False):
     """Sample one token per row of `logits` ([B, V], float32 or float16).
 
     temperature f32[B] (0 = greedy), top_k i32[B] (<= 0 off), top_p f32[B]
@@ -44,7 +45,11 @@ def sample_batch(logits: torch.Tensor, temperature: torch.Tensor, top_k: torch.T
     out_probs, if given, is filled with the post-filter probabilities [B, V].
     row_best, if given, holds the row maxima that `head.lm_head` wrote with
     these logits: greedy rows without a penalty take their token from it.
-    The launch is asynchronous on the current stream.
+    share_rows: the batch may mix rows with top-k off and other rows
+    (MXS_FLAG_SHARE_ROWS: the former share their passes with the
+    workgroups that finished their own rows; see `shares_rows`).  The
+    tokens are the same either way.  The launch is asynchronous on the
+    current stream.
     """
     _native.require_gpu(logits.device)
     ext = _native.extension()
@@ -53,13 +58,22 @@ def sample_batch(logits: torch.Tensor, temperature: torch.Tensor, top_k: torch.T
     tokens = torch.empty(B, dtype=torch.int64, device=dev)
     status = torch.empty(B, dtype=torch.int32, device=dev)
     ws = _native.workspace(dev, B, V)
+    flags = ext.FLAG_SHARE_ROWS if share_rows else 0
     if row_best is None:
         ext.sample(logits, temperature, top_k, top_p, penalty, hist_offsets, hist_ids, uniforms,
-                   tokens, status, out_probs, ws)
+                   tokens, status, out_probs, ws, flags)
     else:
         ext.sample_head(logits, temperature, top_k, top_p, penalty, hist_offsets, hist_ids, uniforms,
-                        tokens, status, out_probs, row_best, ws)
+                        tokens, status, out_probs, row_best, ws, flags)
     return (tokens, status) if return_status else tokens
+
+
+def shares_rows(params_list, V: int) -> bool:
+    """Whether a batch of these SamplingParams mixes rows with top-k off
+    (sampling.py:52: top_k <= 0, or top_k >= V, with a temperature) and
+    other rows: then its top-k-off rows are worth sharing (share_rows)."""
+    off = [p.temperature != 0.0 and (int(p.top_k) <= 0 or int(p.top_k) >= V) for p in params_list]
+    return any(off) and not all(off)
 
 
 class Sampler:
@@ -82,9 +96,10 @@ class Sampler:
                                      dtype=torch.uint8, device=self.device)   # (zero-filled once)
 
     def run(self, logits, temperature, top_k, top_p, penalty, hist_offsets=None,
-            hist_ids=None, uniforms=None):
+            hist_ids=None, uniforms=None, share_rows: bool = False):
         self.ext.sample(logits, temperature, top_k, top_p, penalty, hist_offsets, hist_ids,
-                        uniforms, self.tokens, self.status, self.probs, self.workspace)
+                        uniforms, self.tokens, self.status, self.probs, self.workspace,
+                        self.ext.FLAG_SHARE_ROWS if share_rows else 0)
         return self.tokens
 
 
@@ -158,7 +173,8 @@ def sample_requests(logits: torch.Tensor, params_list, histories, generators=Non
     reference would for the first failing row."""
     B, V = logits.shape
     packed = pack_requests(params_list, histories, V, logits.device, generators)
-    tokens, status = sample_batch(logits, out_probs=out_probs, return_status=True, **packed)
+    tokens, status = sample_batch(logits, out_probs=out_probs, return_status=True,
+                                  share_rows=shares_rows(params_list, V), **packed)
     st = status.cpu().tolist()
     for r, s in enumerate(st):
         if s != ROW_OK:
@@ -171,7 +187,7 @@ def sample_batch_ranges(logits: torch.Tensor, temperature: torch.Tensor, top_k: 
                         hist_end: torch.Tensor, hist_ids: torch.Tensor,
                         uniforms: Optional[torch.Tensor] = None,
                         out_probs: Optional[torch.Tensor] = None,
-                        return_status: bool = False):
+                        return_status: bool = False, share_rows: bool = False):
     """sample_batch with row r's history at hist_ids[hist_begin[r], hist_end[r])
     (i32[B] each, on the device): hist_ids can stay on the device across
     steps (HistoryStore).  The launch is asynchronous on the current stream."""
@@ -183,7 +199,7 @@ def sample_batch_ranges(logits: torch.Tensor, temperature: torch.Tensor, top_k: 
     status = torch.empty(B, dtype=torch.int32, device=dev)
     ws = _native.workspace(dev, B, V)
     ext.sample_ranges(logits, temperature, top_k, top_p, penalty, hist_begin, hist_end, hist_ids,
-                      uniforms, tokens, status, out_probs, ws)
+                      uniforms, tokens, status, out_probs, ws, ext.FLAG_SHARE_ROWS if share_rows else 0)
     return (tokens, status) if return_status else tokens
 
 
@@ -298,7 +314,8 @@ def sample_requests_resident(logits: torch.Tensor, params_list, store: HistorySt
     appending anything."""
     packed = pack_resident(params_list, store, slots, logits.device, generators)
     tokens, status = sample_batch_ranges(logits, hist_ids=store.ids, out_probs=out_probs,
-                                         return_status=True, **packed)
+                                         return_status=True, share_rows=shares_rows(params_list, logits.shape[1]),
+                                         **packed)
     st = status.cpu().tolist()
     for r, s in enumerate(st):
         if s != ROW_OK:

@@ -28,7 +28,7 @@ def declared_functions():
 def header_constants():
     text = open(HEADER).read()
     consts = {k: int(v) for k, v in re.findall(r"\b(MXS_\w+)\s*=\s*(\d+)", text)}
-    consts.update({k: int(v) for k, v in re.findall(r"#define\s+(MXS_\w+)\s+(\d+)", text)})
+    consts.update({k: int(v, 0) for k, v in re.findall(r"#define\s+(MXS_\w+)\s+(0x[0-9a-fA-F]+|\d+)", text)})
     return consts
 
 
@@ -78,6 +78,7 @@ def test_header_constants_match_the_python_layer():
     assert c["MXS_ERR_VOCAB_TOO_LARGE"] == VOCAB and c["MXS_ERR_HIP"] == HIP
     assert c["MXS_ERR_LDS_LIMIT"] == LDS_LIMIT and c["MXS_ERR_SCRATCH_LIMIT"] == SCRATCH_LIMIT
     assert c["MXS_DTYPE_F32"] == 0 and c["MXS_DTYPE_F16"] == 1
+    assert c["MXS_FLAG_SHARE_ROWS"] == 0x100
     assert c["MXS_MAX_VOCAB"] == MAX_VOCAB == batch.MAX_VOCAB
     assert (c["MXS_ROW_OK"], c["MXS_ROW_BAD_HISTORY"], c["MXS_ROW_BAD_PARAM"],
             c["MXS_ROW_NONFINITE"], c["MXS_ROW_EMPTY_NUCLEUS"]) == \
@@ -131,6 +132,8 @@ def test_sample_rejects_bad_arguments_before_launching(lib):
     assert call(lib, V=0) == INVALID
     assert call(lib, V=MAX_VOCAB + 1, ld=MAX_VOCAB + 1) == VOCAB
     assert call(lib, dtype=2) == INVALID
+    assert call(lib, dtype=0x100 | 2) == INVALID      # the sharing flag on an unknown dtype
+    assert call(lib, dtype=0x200) == INVALID          # an unknown flag
     assert call(lib, logits=None) == INVALID
     assert call(lib, temperature=None) == INVALID
     assert call(lib, top_k=None) == INVALID

@@ -1,6 +1,8 @@
 """Top-k-off rows shared with helper workgroups (batches above 64 rows).
 
-In a batch of more than 64 rows that mixes rows with top-k off
+With the flag MXS_FLAG_SHARE_ROWS (share_rows=True; sample_requests sets it
+from the requests' parameters, mi355x_sampler.shares_rows), in an fp32
+batch of more than 64 rows that mixes rows with top-k off
 (sampling.py:56-69 over the whole row) and other rows, the first 16 rows
 with top-k off (by row order) open their two passes to the workgroups that
 finished their own rows; those take slices from the back of each pass and
@@ -82,7 +84,7 @@ def check(oracle, w, tok, st):
 def test_mixed_zipf_batch(oracle, cuda):
     w = make_workload("zipf_k0")
     say(f"[shared] zipf_k0 B={w.B} rows with top-k off: {int((w.top_k <= 0).sum())}")
-    tok, st = sample_batch(**w.to_device(cuda), return_status=True)
+    tok, st = sample_batch(**w.to_device(cuda), return_status=True, share_rows=True)
     torch.cuda.synchronize()
     check(oracle, w, tok, st)
 
@@ -96,9 +98,13 @@ def test_mixed_zipf_batch(oracle, cuda):
 def test_mixed_batches(oracle, cuda, seed, V, B, frac):
     w = mixed(seed, V, B, frac)
     say(f"[shared] seed={seed} V={V} B={B} rows with top-k off: {int(((w.top_k <= 0) | (w.top_k >= V)).sum())}")
-    tok, st = sample_batch(**w.to_device(cuda), return_status=True)
+    d = w.to_device(cuda)
+    tok, st = sample_batch(**d, return_status=True, share_rows=True)
     torch.cuda.synchronize()
     check(oracle, w, tok, st)
+    # the launch without the flag (no sharing code) gives the same tokens
+    tok2, st2 = sample_batch(**d, return_status=True)
+    assert torch.equal(tok, tok2) and torch.equal(st, st2)
 
 
 def test_one_sampler_many_calls(oracle, cuda):
@@ -111,7 +117,7 @@ def test_one_sampler_many_calls(oracle, cuda):
         say(f"[shared] sampler call seed={seed}")
         d = w.to_device(cuda)
         s.run(d["logits"], d["temperature"], d["top_k"], d["top_p"], d["penalty"], d["hist_offsets"],
-              d["hist_ids"], d["uniforms"])
+              d["hist_ids"], d["uniforms"], share_rows=True)
         torch.cuda.synchronize()
         check(oracle, w, s.tokens, s.status)
 
@@ -126,7 +132,7 @@ def test_unaligned_rows(oracle, cuda):
     big[:, :V] = d["logits"]
     d["logits"] = big[:, :V]
     say("[shared] unaligned rows")
-    tok, st = sample_batch(**d, return_status=True)
+    tok, st = sample_batch(**d, return_status=True, share_rows=True)
     torch.cuda.synchronize()
     check(oracle, w, tok, st)
 
@@ -134,6 +140,7 @@ def test_unaligned_rows(oracle, cuda):
 def test_all_rows_top_k_off(oracle, cuda):
     w = mixed(31, 20000, 70, 1.0)
     say("[shared] every row with top-k off")
-    tok, st = sample_batch(**w.to_device(cuda), return_status=True)
+    tok, st = sample_batch(**w.to_device(cuda), return_status=True, share_rows=True)
     torch.cuda.synchronize()
     check(oracle, w, tok, st)
+
