@@ -1639,7 +1639,8 @@ struct WideJob {
     float T, pen, yhi, ylo, scale, m, yca, ycb, yda, ydb;
     uint32_t neg, pen_on;
     uint32_t gmax, gmin;              // pass 1: the helpers' key extremes
-    uint32_t ovf, pad1;               // pass 1: a helper's segment ran full
+    uint32_t ovf;                     // pass 1: a helper's segment ran full
+    uint32_t ver;                     // (job 0's) bumped when a pass opens or a job closes
 };
 static_assert(sizeof(WideJob) <= WJ_HDR, "a job's header");
 static_assert(WJ_S < 256 && WJ_NJOB <= 64, "S fits the tag; one lane per job");
@@ -1658,6 +1659,14 @@ __device__ __forceinline__ u64* wj_kc(WideJob* J, int s) { return wj_top(J, WJ_S
 __device__ __forceinline__ u64* wj_kd(WideJob* J, int s) { return wj_kc(J, WJ_S) + (size_t)s * WJ_WINS; }
 __device__ __forceinline__ uint32_t* wj_cnt(WideJob* J, int list) { return (uint32_t*)wj_kd(J, WJ_S) + list * WJ_S; }
 __device__ __forceinline__ uint32_t* wj_bm(WideJob* J) { return wj_cnt(J, 3); }
+// The records' version (job 0's ver): owners add 1 after a pass opens or a
+// job closes, so that idle helpers poll one word and scan the jobs only when
+// it moves.
+__device__ __forceinline__ void wj_bump(unsigned char* wj)
+{
+    __builtin_amdgcn_s_waitcnt(0);   // (the tag before the version)
+    atomicAdd(&wj_job(wj, 0)->ver, 1u);
+}
 // slice s's pass-2 sums: wb, ac, ad at [0], [WJ_S], [2 WJ_S]
 __device__ __forceinline__ u64* wj_sums(WideJob* J, int s) { return (u64*)(wj_bm(J) + WJ_BMW) + s; }
 __device__ __forceinline__ u64 wj_tag(uint32_t epoch, int S, uint32_t phase)
@@ -2000,7 +2009,10 @@ __device__ __forceinline__ int finish_wide2(const Params& p, int r, RowStream<TI
     auto close_job = [&]() {   // no more slices; helpers leave the job
         if (job >= 0) {
             __syncthreads();
-            if (tid == 0) put_dev64(&J->tag, wj_tag(p.epoch, S, 3u));
+            if (tid == 0) {
+                put_dev64(&J->tag, wj_tag(p.epoch, S, 3u));
+                wj_bump(p.wj);
+            }
             job = -1;
         }
     };
@@ -2031,7 +2043,10 @@ __device__ __forceinline__ int finish_wide2(const Params& p, int r, RowStream<TI
         }
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        if (tid == 0) put_dev64(&J->tag, wj_tag(p.epoch, S, 1u));
+        if (tid == 0) {
+            put_dev64(&J->tag, wj_tag(p.epoch, S, 1u));
+            wj_bump(p.wj);
+        }
     }
     int taken1 = S, taken2 = S;   // the owner's slices of each pass ([taken, S) the helpers')
     if constexpr (!SH) {
@@ -2236,6 +2251,7 @@ __device__ __forceinline__ int finish_wide2(const Params& p, int r, RowStream<TI
         put_devf(&J->yda, yda); put_devf(&J->ydb, ydb);
         __builtin_amdgcn_s_waitcnt(0);
         put_dev64(&J->tag, wj_tag(p.epoch, S, 2u));
+        wj_bump(p.wj);
     }
     if constexpr (!SH) {
         NoClaims fc{S};
@@ -2383,12 +2399,22 @@ __device__ __forceinline__ void help_rows(const Params& p, unsigned char* smem)
         u64* KD = (u64*)(smem + W2_KD);
         RowStream<TIn> rs((const TIn*)p.logits, 0, false);
         int j = -1, phase = 0, s = -1, S = 0;   // the slice in hand (s >= 0)
+        uint32_t seen = 0;                       // (wave 0) the version at the last scan
+        bool rescan = true;                      // (wave 0) scan whatever the version
+        u64 last_lm = 0;                         // (wave 0) the jobs pending at the last scan
         for (int idle = 0; idle < WJ_SPIN;) {
             if (s < 0) {
                 if (w == 0) {
+                    // the records' version: when it has not moved since the last
+                    // scan that found nothing to take, wait (or leave) as then
+                    uint32_t ver = 0;
+                    if (lane == 0) ver = ld_dev(&wj_job(p.wj, 0)->ver);
+                    ver = (uint32_t)__builtin_amdgcn_readfirstlane((int)ver);
+                    const bool scan = rescan || ver != seen;
+                    seen = ver;
                     // lane l: job l's tag and claims
                     u64 tg = 0, qq = 0;
-                    if (lane < WJ_NJOB) {
+                    if (scan && lane < WJ_NJOB) {
                         WideJob* Jl = wj_job(p.wj, lane);
                         tg = ld_dev64(&Jl->tag);
                         qq = ld_dev64((const u64*)&Jl->q1);
@@ -2398,7 +2424,9 @@ __device__ __forceinline__ void help_rows(const Params& p, unsigned char* smem)
                                       ((uint32_t)(tg >> 16) & 0xFFFFu) == WJ_MAGIC && (ph == 1u || ph == 2u);
                     const uint32_t q = ph == 1u ? (uint32_t)qq : (uint32_t)(qq >> 32);
                     const bool open = live && (q & 0xFFFFu) + (q >> 16) < Sl;
-                    const u64 om = __ballot(open), lm = __ballot(live);
+                    const u64 om = __ballot(open), lm = scan ? __ballot(live) : last_lm;
+                    last_lm = lm;
+                    rescan = false;
                     int cmd = -2, cph = 0, cs = -1, cS = 0;
                     if (om) {
                         // this workgroup's last job first, else open job number
@@ -2422,6 +2450,7 @@ __device__ __forceinline__ void help_rows(const Params& p, unsigned char* smem)
                         if (lane < NPAR) hc_par[lane] = pw;
                         cs = (got & 0xFFFFu) + (got >> 16) < (uint32_t)cS ? cS - 1 - (int)(got >> 16) : -1;
                         cmd = pick;   // (a refused claim: scan again at once)
+                        rescan = true;
                     } else if (lm && p.help) {
                         cmd = -1;     // jobs pending: wait
                     }

@@ -180,6 +180,27 @@ def test_request_bodies_through_the_sampler(oracle, cuda):
     assert got == ref.tokens[ok].tolist()
 
 
+def test_large_mixed_request_batch_shares_rows(oracle, cuda):
+    """96 requests that mix the worker's defaults (top-k off) with top-k,
+    greedy and top-p rows: sample_requests sets MXS_FLAG_SHARE_ROWS
+    (shares_rows) and the tokens still equal the oracle's."""
+    from mi355x_sampler import shares_rows
+    kinds = [{}, {"temperature": "0.8", "top_k": "50", "top_p": 0.9, "repetition_penalty": 1.1},
+             {"temperature": 1.3, "top_p": 0.5}, {"temperature": 0}]
+    B = 96
+    params = [params_from_request(kinds[r % len(kinds)]) for r in range(B)]
+    assert shares_rows(params, VOCAB)
+    w = make_workload("zipf", B=B)
+    hists = [w.hist_ids[w.hist_offsets[r]:w.hist_offsets[r + 1]].tolist() for r in range(B)]
+    seeds = [11 * r + 3 for r in range(B)]
+    say("[scheduler] large mixed request batch")
+    ref, _ = expected(oracle, w.logits, params, hists, seeds)
+    assert np.array_equal(ref.status, np.zeros(B, np.int32))
+    gens = [torch.Generator().manual_seed(s) for s in seeds]
+    got = sample_requests(torch.from_numpy(w.logits).to(cuda), params, hists, gens)
+    assert got == ref.tokens.tolist()
+
+
 def bind(path):
     """INTEGRATION.md's ctypes binding of mxs_sample, as written there."""
     lib = ctypes.CDLL(path)
