@@ -2985,22 +2985,41 @@ __device__ __forceinline__ bool finish_counts(const Params& p, int r, RowStream<
         __syncthreads();
         const uint32_t Rd = need_d ? dp.R : 0xFFFFFFFFu, Rc = need_c ? cut.R : 0xFFFFFFFFu;
         const uint32_t zd = Rd == RK_ZERO ? 1u : 0u, zc = Rc == RK_ZERO ? 1u : 0u;   // (rank 0x8000 is 0 too)
+        // A group's raw fp16 patterns, in both halves of P: its value's, or
+        // +0 and -0 for rank RK_ZERO (M masks the sign off); for a group not
+        // looked for, a NaN pattern, which no row that gets here holds.
+        auto pattern = [&](bool need, uint32_t R, uint32_t& P, uint32_t& M) {
+            P = !need ? 0x7E007E00u : (R == RK_ZERO ? 0u : (R ^ (R < 0x8000u ? XA : XB)) * 0x10001u);
+            M = need && R == RK_ZERO ? 0x7FFF7FFFu : 0xFFFFFFFFu;
+        };
+        uint32_t Pd, Md, Pc, Mc;
+        pattern(need_d, Rd, Pd, Md);
+        pattern(need_c, Rc, Pc, Mc);
+        // The elements of a vector that match, a bit each (bits 2k and
+        // 2k + 1: the halves of word k).  Almost no vector holds one, which
+        // a test for a zero half in the four words shows first.
+        auto match8 = [](const RowStream<__half>::vec_t& v, uint32_t P, uint32_t M) -> uint32_t {
+            uint32_t x[4], z = 0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                x[k] = (v[k] ^ P) & M;
+                z |= (x[k] - 0x00010001u) & ~x[k];
+            }
+            uint32_t b = 0;
+            if (z & 0x80008000u) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    b |= ((x[k] & 0xFFFFu) == 0u ? 1u : 0u) << (2 * k) | ((x[k] >> 16) == 0u ? 2u : 0u) << (2 * k);
+            }
+            return b;
+        };
         // the bits of a vector's eight elements, one LDS atomic per bitmap
         // when any is set (elements e .. e + 7 share one bitmap word)
         auto marks = [&](auto both) {
             rs.run_raw(
                 [&](const RowStream<__half>::vec_t& v, int e) {
-                    uint32_t md = 0, mc = 0;
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        const uint32_t Rp = ranks2(v[k]);
-                        md |= ((Rp & 0xFFFFu) - Rd <= zd ? 1u : 0u) << (2 * k);
-                        md |= ((Rp >> 16) - Rd <= zd ? 2u : 0u) << (2 * k);
-                        if constexpr (decltype(both)::value) {
-                            mc |= ((Rp & 0xFFFFu) - Rc <= zc ? 1u : 0u) << (2 * k);
-                            mc |= ((Rp >> 16) - Rc <= zc ? 2u : 0u) << (2 * k);
-                        }
-                    }
+                    const uint32_t md = match8(v, Pd, Md);
+                    const uint32_t mc = decltype(both)::value ? match8(v, Pc, Mc) : 0u;
                     if (md) atomicOr(&Bd[e >> 5], md << (e & 31));
                     if (mc) atomicOr(&Bc[e >> 5], mc << (e & 31));
                 },
