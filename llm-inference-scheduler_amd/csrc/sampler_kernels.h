@@ -2713,7 +2713,7 @@ __device__ __forceinline__ bool finish_counts(const Params& p, int r, RowStream<
         uint4* c4 = (uint4*)smem;
 #pragma unroll
         for (int i = 0; i < KC_CS / 16 / NT; ++i) c4[tid + i * NT] = uint4{0u, 0u, 0u, 0u};
-        if (tid < NCH) HS[tid] = 0;
+        if (tid < NCH) { HS[tid] = 0; CS[tid] = 0; }
         if (tid == 0) { s_csum = 0; s_flag = 0; s_ng = 0; s_own = 0xFFFFFFFFu; }
     }
     __syncthreads();
@@ -2829,20 +2829,30 @@ __device__ __forceinline__ bool finish_counts(const Params& p, int r, RowStream<
     // round-robin to the waves; a wave skips a chunk with no elements)
     {
         uint32_t csum = 0, nanb = 0;
-        for (int c = wave_id(); c < NCH; c += NWAVES) {
-            const uint2 wd = *(const uint2*)&cnt[(RCH / 2) * c + 2 * lane];
-            u64 acc = 0;
-            if (__ballot((wd.x | wd.y) != 0u)) {
-                const uint32_t R0 = (uint32_t)(RCH * c) + 4u * (uint32_t)lane;
-                const uint32_t k0 = wd.x & 0xFFFFu, k1 = wd.x >> 16, k2 = wd.y & 0xFFFFu, k3 = wd.y >> 16;
-                acc = count_mass(k0, val_q(R0) - m) + count_mass(k1, val_q(R0 + 1u) - m) +
-                      count_mass(k2, val_q(R0 + 2u) - m) + count_mass(k3, val_q(R0 + 3u) - m);
-                csum += k0 + k1 + k2 + k3;
-                // (RK_NINF is a multiple of 4: the ranks above it are NaN values)
-                nanb |= R0 > RK_NINF ? (wd.x | wd.y) : (R0 == RK_NINF ? (k1 | wd.y) : 0u);
-                acc = wave_sum_u64(acc);
+        static_assert(NCH % (2 * NWAVES) == 0, "chunk pairs");
+        for (int c2 = wave_id(); c2 < NCH; c2 += 2 * NWAVES) {
+            uint2 wq[2];   // (both chunks' counts requested together)
+#pragma unroll
+            for (int q = 0; q < 2; ++q) wq[q] = *(const uint2*)&cnt[(RCH / 2) * (c2 + q * NWAVES) + 2 * lane];
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const int c = c2 + q * NWAVES;
+                const uint2 wd = wq[q];
+                if (__ballot((wd.x | wd.y) != 0u)) {
+                    const uint32_t R0 = (uint32_t)(RCH * c) + 4u * (uint32_t)lane;
+                    const uint32_t k0 = wd.x & 0xFFFFu, k1 = wd.x >> 16, k2 = wd.y & 0xFFFFu, k3 = wd.y >> 16;
+                    u64 acc = count_mass(k0, val_q(R0) - m) + count_mass(k1, val_q(R0 + 1u) - m) +
+                              count_mass(k2, val_q(R0 + 2u) - m) + count_mass(k3, val_q(R0 + 3u) - m);
+                    csum += k0 + k1 + k2 + k3;
+                    // (RK_NINF is a multiple of 4: the ranks above it are NaN values)
+                    nanb |= R0 > RK_NINF ? (wd.x | wd.y) : (R0 == RK_NINF ? (k1 | wd.y) : 0u);
+                    // the sums of the wave's four rows of 16 lanes (every sum
+                    // of masses is below 2^63), added into the chunk's total
+#pragma unroll
+                    for (int step = 0; step < 4; ++step) acc += dpp_step(acc, 0ull, step);
+                    if ((lane & 15) == 15) atomicAdd((unsigned long long*)&CS[c], (unsigned long long)acc);
+                }
             }
-            if (lane == 0) CS[c] = acc;
         }
         csum = wave_sum_u32(csum);
         if (lane == 0) atomicAdd(&s_csum, csum);
