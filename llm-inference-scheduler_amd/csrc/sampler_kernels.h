@@ -1210,20 +1210,23 @@ struct RowStream {
                 vec(b[j], vi * VW);
             }
         };
+        vec_t C[FU], D[FU];   // (four tiles in flight: the passes over fp16 rows wait on latency)
+        load(C, 2);
+        load(D, 3);
         int t = 0;
-        for (; t + 1 < nfull; t += 2) {
+        for (; t + 3 < ntile; t += 4) {
             words(A, t, false);
-            load(A, t + 2);
+            load(A, t + 4);
             words(Bf, t + 1, false);
-            load(Bf, t + 3);
-        }
-        if (t < nfull) {
-            words(A, t, false);
-            ++t;
-#pragma unroll
-            for (int j = 0; j < FU; ++j) A[j] = Bf[j];
+            load(Bf, t + 5);
+            words(C, t + 2, false);
+            load(C, t + 6);
+            words(D, t + 3, true);
+            load(D, t + 7);
         }
         if (t < ntile) words(A, t, true);
+        if (t + 1 < ntile) words(Bf, t + 1, true);
+        if (t + 2 < ntile) words(C, t + 2, true);
         for (int e = nvec * VW + tid; e < V; e += NT) one((uint32_t)__builtin_bit_cast(uint16_t, rowp[e]), e);
     }
 };
