@@ -24,6 +24,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import platform
 import sys
 import time
@@ -137,16 +138,27 @@ def margin_parity(w, ref, dev, max_rows: int) -> dict:
 
 def load_traffic(workload: str, B: int):
     """HBM bytes per call from the committed rocprofv3 counter summary
-    (FETCH_SIZE and WRITE_SIZE, each scaled by a plain copy's reading)."""
-    path = os.path.join(ROOT, "profiles", f"{workload}_B{B}_hbm_traffic.md")
+    (FETCH_SIZE and WRITE_SIZE, each scaled by a plain copy's reading), and
+    the kernel's average duration in the trace summary of the same build."""
+    base = os.path.join(ROOT, "profiles", f"{workload}_B{B}")
+    traffic = prof_us = None
     try:
-        with open(path) as f:
+        with open(base + "_hbm_traffic.md") as f:
             for line in f:
                 if line.startswith("hbm_bytes_per_launch:"):
-                    return int(line.split(":", 1)[1])
+                    traffic = int(line.split(":", 1)[1])
     except (OSError, ValueError):
         pass
-    return None
+    try:
+        with open(base + "_kernel_stats.md") as f:
+            for line in f:
+                m = re.search(r"averages ([0-9.]+) us per launch", line)
+                if m:
+                    prof_us = float(m.group(1))
+                    break
+    except OSError:
+        pass
+    return traffic, prof_us
 
 
 def copy_calibration(dev, nbytes: int, steps: int, warmup: int):
@@ -402,7 +414,10 @@ def main():
     achieved = algo / (mean_us * 1e-6) / 1e9
     rows_per_s = w.B / (ms_per_step * 1e-3)
     dtype = "fp16->fp32" if w.logits.dtype == np.float16 else "fp32"
-    traffic = load_traffic(args.workload, w.B)
+    traffic, prof_us = load_traffic(args.workload, w.B)
+    # the counters describe the kernel as profiled: when the live kernel
+    # time has moved by more than 10 % from the profiled one, they are stale
+    stale = traffic is not None and (prof_us is None or abs(prof_us - mean_us) > 0.1 * mean_us)
     out = {
         "metric": METRIC,
         "value": rows_per_s,
@@ -438,7 +453,8 @@ def main():
                                    "p10": float(np.percentile(dur_us, 10)),
                                    "p90": float(np.percentile(dur_us, 90))}},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
+                     "frac": achieved / HBM_PEAK_GBPS, "traffic": None if stale else traffic,
+                     "traffic_profile": {"kernel_us": prof_us, "hbm_bytes": traffic, "stale": stale},
                      "algorithmic_bytes_per_launch": algo,
                      "kernel": "k_fused (one workgroup per row), one mxs_sample call"},
         "cold_mall": cold,
